@@ -1,0 +1,126 @@
+/*
+ * C ABI of the MI355X attention hot path (libruntherder_attn.so).
+ *
+ * Every entry point takes plain device pointers, host int sizes and a HIP
+ * stream passed as void* (NULL = the null stream), enqueues its work
+ * asynchronously, never synchronizes and never allocates, so calls are
+ * HIP-graph capturable. Return value: RTH_OK, or an error code with a message
+ * available from rth_last_error_string() (thread-local).
+ *
+ * Element types at the boundary:
+ *   bf16  -> uint16_t (raw bfloat16 bits)
+ *   E4M3  -> uint8_t  (OCP FP8 E4M3FN: bias 7, max 448, 0x7F/0xFF NaN)
+ *
+ * Layouts follow the reference engine (reference paths):
+ *   q, out   [n_new, num_q_heads, head_dim] bf16           (backend.h:31-41)
+ *   k, v     [max_seq_len, num_kv_heads, head_dim] E4M3   (kv_view.h:7-13)
+ *   k_scale, v_scale [max_seq_len, num_kv_heads] fp32, one dequant scale per
+ *            (token, kv_head); value = float(code) * scale  (kv_view.h:7-13)
+ *   cache_len / at_pos are DEVICE-resident ints, unchecked against the cache
+ *   size (the caller owns that bound), as in the reference.
+ */
+#ifndef RTH_ATTN_H
+#define RTH_ATTN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+    RTH_OK              = 0,
+    RTH_ERR_INVALID_ARG = 1, /* argument check failed (message says which) */
+    RTH_ERR_HIP         = 2, /* HIP runtime / launch error */
+};
+
+/* Message of the last failing call on this thread ("" if none). */
+const char* rth_last_error_string(void);
+
+/* Replaces kernels::quantize_kv_fp8 (reference
+ * include/runtherder/kernels/quantization.cuh:50-57). Per row of head_dim bf16:
+ * scale = amax/448, q = E4M3_satfinite(x * (448/amax)); row r is written at
+ * destination row r + (*at_pos) * rows_per_pos. head_dim % 8 == 0,
+ * 8 <= head_dim <= 16384. Bit-exact with the reference's arithmetic. */
+int rth_kv_quantize_fp8(uint8_t* q, float* scale, const uint16_t* x,
+                        const int* at_pos, int rows_per_pos, int num_rows,
+                        int head_dim, void* stream);
+
+/* Given-scale variant (no reference counterpart): scale[dst] is an input and
+ * q = E4M3_satfinite(x * (1/scale[dst])). Used to fill caches whose scales are
+ * set by the caller (e.g. per-head calibration). Same constraints. */
+int rth_kv_quantize_fp8_scaled(uint8_t* q, const float* scale,
+                               const uint16_t* x, const int* at_pos,
+                               int rows_per_pos, int num_rows, int head_dim,
+                               void* stream);
+
+/* Replaces the two quantize_kv_fp8 launches of engine::KVCache::append
+ * (reference include/runtherder/engine/kv_cache.h:62-78) with one launch:
+ * quantizes k and v ([n_new, num_kv_heads, head_dim] bf16) into one layer's
+ * slabs at rows *at_pos .. *at_pos + n_new - 1. */
+int rth_kv_append_fp8(uint8_t* k_cache, uint8_t* v_cache, float* k_scale,
+                      float* v_scale, const uint16_t* k, const uint16_t* v,
+                      const int* at_pos, int n_new, int num_kv_heads,
+                      int head_dim, void* stream);
+
+/* Replaces kernels::flash_split_scratch_floats (reference
+ * include/runtherder/kernels/flash_decode.cuh:16-24): floats of decode
+ * scratch for max_splits splits. Layout: [Hq*S] m, [Hq*S] l, [Hq*S*D] acc as
+ * in the reference, followed by one int arrival counter per kv head. */
+size_t rth_split_scratch_floats(int num_q_heads, int head_dim, int max_splits);
+
+/* Zeroes the arrival counters of a decode scratch (once, after allocation;
+ * rth_attn_decode_split leaves them zeroed after every call). No counterpart
+ * in the reference, whose scratch needs no initialization. */
+int rth_split_scratch_init(float* partial, int num_q_heads, int head_dim,
+                           int max_splits, void* stream);
+
+/* Split count AdaptiveAttention uses on `device` for num_kv_heads kv heads:
+ * enough (kv head, split) workgroups to fill every compute unit. */
+int rth_default_num_splits(int num_kv_heads, int device);
+
+/* Replaces kernels::flash_decode_split_bf16 (reference
+ * include/runtherder/kernels/flash_decode.cuh:45-59): one query token,
+ * attends *cache_len + 1 keys, split-K over num_splits key ranges with a
+ * log-sum-exp merge. `partial` is caller-owned scratch of
+ * rth_split_scratch_floats(Hq, D, num_splits) floats whose counters were
+ * zeroed once by rth_split_scratch_init. head_dim in {32,64,128,256,512};
+ * 64/128/256 with Hq/Hkv <= 16 run the MFMA kernel, the rest the naive one. */
+int rth_attn_decode_split(uint16_t* out, const uint16_t* q, const uint8_t* k,
+                          const uint8_t* v, const float* k_scale,
+                          const float* v_scale, float* partial, int num_splits,
+                          const int* cache_len, int num_q_heads,
+                          int num_kv_heads, int head_dim, float scale,
+                          void* stream);
+
+/* Replaces kernels::flash_prefill_bf16 (reference
+ * include/runtherder/kernels/flash_prefill.cuh:26-39): causal attention of
+ * n_new queries at positions *cache_len .. *cache_len + n_new - 1 over keys
+ * 0 .. *cache_len + n_new - 1. head_dim == 128. */
+int rth_attn_prefill(uint16_t* out, const uint16_t* q, const uint8_t* k,
+                     const uint8_t* v, const float* k_scale,
+                     const float* v_scale, int n_new, const int* cache_len,
+                     int num_q_heads, int num_kv_heads, int head_dim,
+                     float scale, void* stream);
+
+/* Replaces kernels::attention_causal_bf16 (reference
+ * include/runtherder/kernels/attention.cuh:21-34): the same causal attention
+ * as rth_attn_prefill at any n_new, by the plain two-pass algorithm.
+ * head_dim <= 512. */
+int rth_attn_naive(uint16_t* out, const uint16_t* q, const uint8_t* k,
+                   const uint8_t* v, const float* k_scale, const float* v_scale,
+                   int n_new, const int* cache_len, int num_q_heads,
+                   int num_kv_heads, int head_dim, float scale, void* stream);
+
+/* *pos += delta on device. No counterpart in the reference (which advances
+ * the decode position with a host copy, reference
+ * include/runtherder/engine/context.h:41-45); lets one captured graph hold
+ * several decode steps. */
+int rth_advance_position(int* pos, int delta, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* RTH_ATTN_H */

@@ -1,0 +1,36 @@
+// Plain two-pass causal attention with the reference signature (reference
+// include/runtherder/kernels/attention.cuh:21-34), forwarding to the C ABI.
+#pragma once
+
+#include <hip/hip_bf16.h>
+#include <hip/hip_fp8.h>
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+#include <rth_attn.h>
+#include <runtherder/device/check.h>
+
+namespace runtherder::kernels {
+
+inline void attention_causal_bf16(__hip_bfloat16*       out,
+                                  const __hip_bfloat16* q,
+                                  const __hip_fp8_e4m3* k,
+                                  const __hip_fp8_e4m3* v,
+                                  const float*          k_scale,
+                                  const float*          v_scale,
+                                  int                   n_new,
+                                  const int*            cache_len,
+                                  int                   num_q_heads,
+                                  int                   num_kv_heads,
+                                  int                   head_dim,
+                                  float                 scale,
+                                  hipStream_t           stream = nullptr) {
+    RUNTHERDER_RTH_CHECK(rth_attn_naive(
+        reinterpret_cast<std::uint16_t*>(out), reinterpret_cast<const std::uint16_t*>(q),
+        reinterpret_cast<const std::uint8_t*>(k), reinterpret_cast<const std::uint8_t*>(v),
+        k_scale, v_scale, n_new, cache_len, num_q_heads, num_kv_heads, head_dim, scale,
+        stream));
+}
+
+}  // namespace runtherder::kernels

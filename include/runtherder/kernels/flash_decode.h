@@ -1,0 +1,55 @@
+// Split-K flash decode with the reference signature (reference
+// include/runtherder/kernels/flash_decode.cuh:16-59), forwarding to the C ABI.
+#pragma once
+
+#include <hip/hip_bf16.h>
+#include <hip/hip_fp8.h>
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+
+#include <rth_attn.h>
+#include <runtherder/device/check.h>
+
+namespace runtherder::kernels {
+
+// Floats of decode scratch for max_splits splits: the reference's m, l, acc
+// slab followed by one arrival counter per kv head. Zero the counters once
+// with init_flash_split_scratch after allocating.
+[[nodiscard]] inline std::size_t flash_split_scratch_floats(int num_q_heads, int head_dim,
+                                                            int max_splits) {
+    return rth_split_scratch_floats(num_q_heads, head_dim, max_splits);
+}
+
+inline void init_flash_split_scratch(float* partial, int num_q_heads, int head_dim,
+                                     int max_splits, hipStream_t stream = nullptr) {
+    RUNTHERDER_RTH_CHECK(
+        rth_split_scratch_init(partial, num_q_heads, head_dim, max_splits, stream));
+}
+
+// One query token attends *cache_len + 1 keys in num_splits key ranges merged by
+// log-sum-exp. The split reassociates the float accumulation and can differ
+// from a serial accumulation in the last bits, not in value.
+inline void flash_decode_split_bf16(__hip_bfloat16*       out,
+                                    const __hip_bfloat16* q,
+                                    const __hip_fp8_e4m3* k,
+                                    const __hip_fp8_e4m3* v,
+                                    const float*          k_scale,
+                                    const float*          v_scale,
+                                    float*                partial,
+                                    int                   num_splits,
+                                    const int*            cache_len,
+                                    int                   num_q_heads,
+                                    int                   num_kv_heads,
+                                    int                   head_dim,
+                                    float                 scale,
+                                    hipStream_t           stream = nullptr) {
+    RUNTHERDER_RTH_CHECK(rth_attn_decode_split(
+        reinterpret_cast<std::uint16_t*>(out), reinterpret_cast<const std::uint16_t*>(q),
+        reinterpret_cast<const std::uint8_t*>(k), reinterpret_cast<const std::uint8_t*>(v),
+        k_scale, v_scale, partial, num_splits, cache_len, num_q_heads, num_kv_heads, head_dim,
+        scale, stream));
+}
+
+}  // namespace runtherder::kernels

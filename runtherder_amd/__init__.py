@@ -1,0 +1,30 @@
+"""MI355X-native attention hot path of the Runtherder engine.
+
+Hand-written gfx950 HIP kernels (causal flash prefill on bf16 MFMA, split-K
+GQA flash decode, FP8 E4M3 KV append/quantize) behind a C ABI
+(include/rth_attn.h, libruntherder_attn.so), with the reference engine's
+C++20 interface in include/runtherder/ and a torch-tensor front end in
+runtherder_amd.ops.
+"""
+from . import _ffi
+from .ops import (  # noqa: F401
+    AdaptiveAttention,
+    AttentionBackend,
+    AttnConfig,
+    BackendKind,
+    KVCache,
+    KVView,
+    NaiveAttention,
+    advance_position,
+    attention_causal_bf16,
+    default_num_splits,
+    flash_decode_split_bf16,
+    flash_prefill_bf16,
+    flash_split_scratch_floats,
+    make_attention_backend,
+    new_flash_split_scratch,
+    quantize_kv_fp8,
+    quantize_kv_fp8_scaled,
+)
+
+LIB_PATH = _ffi.LIB_PATH

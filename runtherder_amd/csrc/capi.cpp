@@ -1,0 +1,233 @@
+// extern "C" boundary of libruntherder_attn.so (declared in include/rth_attn.h).
+//
+// Argument checks mirror the reference's launch-site RUNTHERDER_CHECKs
+// (reference src/kernels/flash_decode.cu:286-291, flash_prefill.cu:226-228,
+// attention.cu:109-116, quantization.cu:348-352) but report through return
+// codes and rth_last_error_string() instead of exiting the process.
+#include <hip/hip_runtime.h>
+
+#include <cstdio>
+#include <cstring>
+#include <string>
+
+#include "../../include/rth_attn.h"
+#include "launch.hpp"
+
+namespace rth {
+bool decode_mfma_supported(int num_q_heads, int num_kv_heads, int head_dim);
+}
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const std::string& msg) {
+    g_last_error = msg;
+    return code;
+}
+
+int check_hip(hipError_t e, const char* where) {
+    if (e != hipSuccess) {
+        return fail(RTH_ERR_HIP, std::string(where) + ": " + hipGetErrorString(e));
+    }
+    g_last_error.clear();
+    return RTH_OK;
+}
+
+#define RTH_REQUIRE(cond, msg)                        \
+    do {                                              \
+        if (!(cond)) {                                \
+            return fail(RTH_ERR_INVALID_ARG, (msg));  \
+        }                                             \
+    } while (0)
+
+hipStream_t as_stream(void* s) { return static_cast<hipStream_t>(s); }
+
+int check_heads(int num_q_heads, int num_kv_heads) {
+    RTH_REQUIRE(num_q_heads >= 1, "num_q_heads must be >= 1");
+    RTH_REQUIRE(num_kv_heads >= 1, "num_kv_heads must be >= 1");
+    RTH_REQUIRE(num_q_heads % num_kv_heads == 0,
+                "num_q_heads must be divisible by num_kv_heads");
+    return RTH_OK;
+}
+
+int check_quant(const void* q, const void* scale, const void* x, const int* at_pos,
+                int rows_per_pos, int num_rows, int head_dim) {
+    RTH_REQUIRE(q != nullptr && scale != nullptr && x != nullptr,
+                "q, scale and x must not be null");
+    RTH_REQUIRE(num_rows >= 1, "num_rows must be >= 1");
+    RTH_REQUIRE(at_pos != nullptr, "at_pos must not be null");
+    RTH_REQUIRE(rows_per_pos >= 1, "rows_per_pos must be >= 1");
+    RTH_REQUIRE(head_dim >= 8, "head_dim must be >= 8");
+    RTH_REQUIRE(head_dim % 8 == 0, "head_dim must be divisible by 8");
+    RTH_REQUIRE(head_dim <= 16384, "head_dim too large for current dispatch");
+    return RTH_OK;
+}
+
+int check_attn(const void* out, const void* q, const void* k, const void* v,
+               const void* ks, const void* vs, const int* cache_len) {
+    RTH_REQUIRE(out != nullptr && q != nullptr, "out and q must not be null");
+    RTH_REQUIRE(k != nullptr && v != nullptr && ks != nullptr && vs != nullptr,
+                "k, v, k_scale and v_scale must not be null");
+    RTH_REQUIRE(cache_len != nullptr, "cache_len must not be null");
+    return RTH_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* rth_last_error_string(void) { return g_last_error.c_str(); }
+
+int rth_kv_quantize_fp8(uint8_t* q, float* scale, const uint16_t* x,
+                        const int* at_pos, int rows_per_pos, int num_rows,
+                        int head_dim, void* stream) {
+    if (int rc = check_quant(q, scale, x, at_pos, rows_per_pos, num_rows, head_dim)) {
+        return rc;
+    }
+    return check_hip(rth::quantize_kv_fp8_launch(q, scale, x, at_pos, rows_per_pos,
+                                                 num_rows, head_dim, as_stream(stream)),
+                     "rth_kv_quantize_fp8");
+}
+
+int rth_kv_quantize_fp8_scaled(uint8_t* q, const float* scale,
+                               const uint16_t* x, const int* at_pos,
+                               int rows_per_pos, int num_rows, int head_dim,
+                               void* stream) {
+    if (int rc = check_quant(q, scale, x, at_pos, rows_per_pos, num_rows, head_dim)) {
+        return rc;
+    }
+    return check_hip(rth::quantize_kv_fp8_scaled_launch(q, scale, x, at_pos, rows_per_pos,
+                                                        num_rows, head_dim,
+                                                        as_stream(stream)),
+                     "rth_kv_quantize_fp8_scaled");
+}
+
+int rth_kv_append_fp8(uint8_t* k_cache, uint8_t* v_cache, float* k_scale,
+                      float* v_scale, const uint16_t* k, const uint16_t* v,
+                      const int* at_pos, int n_new, int num_kv_heads,
+                      int head_dim, void* stream) {
+    RTH_REQUIRE(n_new >= 1, "KVCache append n_new must be >= 1");
+    RTH_REQUIRE(num_kv_heads >= 1, "num_kv_heads must be >= 1");
+    RTH_REQUIRE(k_cache != nullptr && v_cache != nullptr && k_scale != nullptr &&
+                    v_scale != nullptr && k != nullptr && v != nullptr,
+                "cache slabs, scales and inputs must not be null");
+    if (int rc = check_quant(k_cache, k_scale, k, at_pos, num_kv_heads,
+                             n_new * num_kv_heads, head_dim)) {
+        return rc;
+    }
+    return check_hip(rth::kv_append_fp8_launch(k_cache, v_cache, k_scale, v_scale, k, v,
+                                               at_pos, num_kv_heads, n_new * num_kv_heads,
+                                               head_dim, as_stream(stream)),
+                     "rth_kv_append_fp8");
+}
+
+size_t rth_split_scratch_floats(int num_q_heads, int head_dim, int max_splits) {
+    if (num_q_heads < 1 || head_dim < 1 || max_splits < 1) {
+        return 0;
+    }
+    return rth::decode_scratch_floats(num_q_heads, head_dim, max_splits);
+}
+
+int rth_split_scratch_init(float* partial, int num_q_heads, int head_dim,
+                           int max_splits, void* stream) {
+    RTH_REQUIRE(partial != nullptr, "partial must not be null");
+    RTH_REQUIRE(num_q_heads >= 1 && head_dim >= 1 && max_splits >= 1,
+                "num_q_heads, head_dim and max_splits must be >= 1");
+    return check_hip(rth::decode_scratch_reset_launch(partial, num_q_heads, head_dim,
+                                                      max_splits, as_stream(stream)),
+                     "rth_split_scratch_init");
+}
+
+int rth_default_num_splits(int num_kv_heads, int device) {
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) !=
+            hipSuccess ||
+        cus < 1) {
+        cus = 256;
+    }
+    if (num_kv_heads < 1) {
+        num_kv_heads = 1;
+    }
+    // One 8-wave (kv head, split) workgroup per compute unit, rounded to a
+    // multiple of 8 splits so the XCD-aware mapping applies.
+    int s = (cus + num_kv_heads - 1) / num_kv_heads;
+    s     = (s + 7) / 8 * 8;
+    return s < 8 ? 8 : s;
+}
+
+int rth_attn_decode_split(uint16_t* out, const uint16_t* q, const uint8_t* k,
+                          const uint8_t* v, const float* k_scale,
+                          const float* v_scale, float* partial, int num_splits,
+                          const int* cache_len, int num_q_heads,
+                          int num_kv_heads, int head_dim, float scale,
+                          void* stream) {
+    if (int rc = check_attn(out, q, k, v, k_scale, v_scale, cache_len)) {
+        return rc;
+    }
+    RTH_REQUIRE(num_splits >= 1, "num_splits must be >= 1");
+    if (int rc = check_heads(num_q_heads, num_kv_heads)) {
+        return rc;
+    }
+    RTH_REQUIRE(head_dim == 32 || head_dim == 64 || head_dim == 128 || head_dim == 256 ||
+                    head_dim == 512,
+                "head_dim must be one of 32, 64, 128, 256, 512");
+    if (rth::decode_mfma_supported(num_q_heads, num_kv_heads, head_dim)) {
+        RTH_REQUIRE(partial != nullptr, "partial must not be null");
+        return check_hip(rth::flash_decode_launch(out, q, k, v, k_scale, v_scale, partial,
+                                                  num_splits, cache_len, num_q_heads,
+                                                  num_kv_heads, head_dim, scale,
+                                                  as_stream(stream)),
+                         "rth_attn_decode_split");
+    }
+    return check_hip(rth::attention_naive_launch(out, q, k, v, k_scale, v_scale, 1,
+                                                 cache_len, num_q_heads, num_kv_heads,
+                                                 head_dim, scale, as_stream(stream)),
+                     "rth_attn_decode_split");
+}
+
+int rth_attn_prefill(uint16_t* out, const uint16_t* q, const uint8_t* k,
+                     const uint8_t* v, const float* k_scale,
+                     const float* v_scale, int n_new, const int* cache_len,
+                     int num_q_heads, int num_kv_heads, int head_dim,
+                     float scale, void* stream) {
+    if (int rc = check_attn(out, q, k, v, k_scale, v_scale, cache_len)) {
+        return rc;
+    }
+    RTH_REQUIRE(head_dim == 128, "flash_prefill_bf16 supports head_dim 128 only");
+    RTH_REQUIRE(n_new >= 1, "n_new must be >= 1");
+    if (int rc = check_heads(num_q_heads, num_kv_heads)) {
+        return rc;
+    }
+    return check_hip(rth::flash_prefill_launch(out, q, k, v, k_scale, v_scale, n_new,
+                                               cache_len, num_q_heads, num_kv_heads,
+                                               head_dim, scale, as_stream(stream)),
+                     "rth_attn_prefill");
+}
+
+int rth_attn_naive(uint16_t* out, const uint16_t* q, const uint8_t* k,
+                   const uint8_t* v, const float* k_scale, const float* v_scale,
+                   int n_new, const int* cache_len, int num_q_heads,
+                   int num_kv_heads, int head_dim, float scale, void* stream) {
+    if (int rc = check_attn(out, q, k, v, k_scale, v_scale, cache_len)) {
+        return rc;
+    }
+    RTH_REQUIRE(n_new >= 1, "n_new must be >= 1");
+    if (int rc = check_heads(num_q_heads, num_kv_heads)) {
+        return rc;
+    }
+    RTH_REQUIRE(head_dim >= 1, "head_dim must be >= 1");
+    RTH_REQUIRE(head_dim <= 512, "head_dim exceeds the naive kernel's maximum (512)");
+    return check_hip(rth::attention_naive_launch(out, q, k, v, k_scale, v_scale, n_new,
+                                                 cache_len, num_q_heads, num_kv_heads,
+                                                 head_dim, scale, as_stream(stream)),
+                     "rth_attn_naive");
+}
+
+int rth_advance_position(int* pos, int delta, void* stream) {
+    RTH_REQUIRE(pos != nullptr, "pos must not be null");
+    return check_hip(rth::advance_position_launch(pos, delta, as_stream(stream)),
+                     "rth_advance_position");
+}
+
+}  // extern "C"

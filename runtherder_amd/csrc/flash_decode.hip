@@ -1,0 +1,455 @@
+// Split-K GQA flash decode over an OCP E4M3 KV cache, gfx950.
+//
+// Math follows flash_decode_split_bf16 (reference src/kernels/
+// flash_decode.cu:118-325): per split an online softmax over its key range,
+// then a log-sum-exp merge of the splits, bf16 RNE output. The MI355X design
+// differs from the reference's one-block-per-q-head layout:
+//
+//  * One workgroup per (kv head, split) serves the whole GQA group, so every
+//    K/V byte is read from HBM once, not Hq/Hkv times.
+//  * Scores and the value product run on bf16 MFMA (v_mfma_f32_16x16x32_bf16)
+//    with the GQA group as the 16-wide N dimension: S^T = K Q^T, then
+//    O^T += V^T P^T. E4M3 codes convert exactly to bf16 in registers
+//    (v_cvt_scalef32_pk_bf16_fp8); the per-(token, kv_head) scales are folded
+//    in fp32 into the score column (k_scale) and into P (v_scale).
+//  * K is loaded with 16-byte lane loads along head_dim; V is loaded 8 bytes
+//    per (key, lane) and transposed in registers with v_perm so P^T needs no
+//    cross-lane movement.
+//  * Softmax runs in base 2 (scores pre-multiplied by scale*log2(e)); the
+//    running-max rescale of the accumulator is skipped when no lane's max
+//    moved.
+//  * The split merge is fused: each workgroup writes its (m, l, O) partial,
+//    and the last workgroup of a kv head to arrive (device-scope counter)
+//    merges all splits and writes the output, then re-arms the counter.
+//  * Workgroups of one split for all kv heads land on one XCD, so the
+//    interleaved [token, kv_head] scale lines are fetched into one L2.
+//
+// The key range of split si is [si*per, min(si*per+per, n_keys)) with
+// per = 32 * ceil(ceil(n_keys / S) / 32); splits past the last key exit
+// before touching the counter. n_keys = *cache_len + 1 is read on device, so
+// one launch configuration serves every decode step (graph capturable).
+#include "device_common.hpp"
+#include "launch.hpp"
+
+namespace rth {
+namespace {
+
+constexpr int kDecWaves   = 8;
+constexpr int kDecThreads = kDecWaves * kWave;
+constexpr int kTileKeys   = 32;     // keys per wave iteration (two 16-key MFMAs)
+constexpr int kMaxGroupD  = 2048;   // G * head_dim bound of the LDS wave merge
+
+template <int D>
+struct DecTraits {
+    static_assert(D == 64 || D == 128 || D == 256, "decode MFMA path: D in {64,128,256}");
+    static constexpr int kKChunks = D / 64;   // 16-byte K loads per lane per key
+    static constexpr int kKSteps  = D / 32;   // MFMA k-steps of S^T
+    static constexpr int kVBytes  = D / 16;   // V bytes per lane per key
+    static constexpr int kVWords  = kVBytes / 4;
+    static constexpr int kOMfma   = D / 16;   // PV MFMAs, one per d offset c
+};
+
+// One tile's raw global data held by a lane.
+template <int D>
+struct TileRaw {
+    u32x4    kraw[2][DecTraits<D>::kKChunks];
+    uint32_t vraw[8][DecTraits<D>::kVWords];
+    float    sc;
+};
+
+__device__ __forceinline__ int key_of(int g, int j) {  // P^T k-index -> key in tile
+    return (j < 4) ? (4 * g + j) : (16 + 4 * g + (j - 4));
+}
+
+template <int D>
+__device__ __forceinline__ void load_tile(TileRaw<D>& t, const uint8_t* __restrict__ k,
+                                          const uint8_t* __restrict__ v,
+                                          const float* __restrict__ ks,
+                                          const float* __restrict__ vs, int kb,
+                                          int k1, int kvh, int hkv, int lane) {
+    using T     = DecTraits<D>;
+    const int n = lane & 15;
+    const int g = lane >> 4;
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+        const int      key = min(kb + 16 * u + n, k1 - 1);
+        const uint8_t* kr  = k + (static_cast<int64_t>(key) * hkv + kvh) * D;
+#pragma unroll
+        for (int c = 0; c < T::kKChunks; ++c) {
+            t.kraw[u][c] = *reinterpret_cast<const u32x4*>(kr + 16 * g + 64 * c);
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const int      key = min(kb + key_of(g, j), k1 - 1);
+        const uint8_t* vr  = v + (static_cast<int64_t>(key) * hkv + kvh) * D + T::kVBytes * n;
+        if constexpr (T::kVWords == 1) {
+            t.vraw[j][0] = *reinterpret_cast<const uint32_t*>(vr);
+        } else if constexpr (T::kVWords == 2) {
+            const u32x2 w = *reinterpret_cast<const u32x2*>(vr);
+            t.vraw[j][0]  = w.x;
+            t.vraw[j][1]  = w.y;
+        } else {
+            const u32x4 w = *reinterpret_cast<const u32x4*>(vr);
+            t.vraw[j][0]  = w.x;
+            t.vraw[j][1]  = w.y;
+            t.vraw[j][2]  = w.z;
+            t.vraw[j][3]  = w.w;
+        }
+    }
+    {
+        const int key = min(kb + (lane & 31), k1 - 1);
+        const int64_t row = static_cast<int64_t>(key) * hkv + kvh;
+        t.sc = (lane < 32) ? ks[row] : vs[row];
+    }
+}
+
+template <int D>
+__global__ __launch_bounds__(kDecThreads) void flash_decode_kernel(
+    uint16_t* __restrict__ out, const uint16_t* __restrict__ q,
+    const uint8_t* __restrict__ k, const uint8_t* __restrict__ v,
+    const float* __restrict__ ks, const float* __restrict__ vs,
+    float* __restrict__ partial, int num_splits, const int* __restrict__ cache_len,
+    int hq, int hkv, float scale_log2) {
+    using T = DecTraits<D>;
+
+    __shared__ float sm_sc[kDecWaves][64];
+    __shared__ float sm_m[kDecWaves][16];
+    __shared__ float sm_l[kDecWaves][16];
+    __shared__ float sm_o[kDecWaves * kMaxGroupD];
+    __shared__ int   sm_last;
+
+    const int G    = hq / hkv;
+    const int tid  = static_cast<int>(threadIdx.x);
+    const int wave = tid / kWave;
+    const int lane = tid & (kWave - 1);
+    const int n    = lane & 15;
+    const int g    = lane >> 4;
+
+    // XCD-aware block mapping: all kv heads of one split share bid % 8.
+    const int bid = static_cast<int>(blockIdx.x);
+    int       si, kvh;
+    if ((num_splits & 7) == 0) {
+        const int r = bid >> 3;
+        si          = (r / hkv) * 8 + (bid & 7);
+        kvh         = r % hkv;
+    } else {
+        si  = bid / hkv;
+        kvh = bid % hkv;
+    }
+
+    const int n_keys = *cache_len + 1;
+    int       per    = (n_keys + num_splits - 1) / num_splits;
+    per              = (per + kTileKeys - 1) & ~(kTileKeys - 1);
+    const int n_eff  = (n_keys + per - 1) / per;
+    if (si >= n_eff) {
+        return;
+    }
+    const int k0      = si * per;
+    const int k1      = min(k0 + per, n_keys);
+    const int n_tiles = (k1 - k0 + kTileKeys - 1) / kTileKeys;
+
+    // Q^T as the B operand: column n = q head of the group (zero past G).
+    bf16x8 qop[T::kKSteps];
+    {
+        const bool      has = n < G;
+        const uint16_t* qr  = q + static_cast<int64_t>(kvh * G + (has ? n : 0)) * D;
+#pragma unroll
+        for (int c = 0; c < T::kKChunks; ++c) {
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                u32x4 w = *reinterpret_cast<const u32x4*>(qr + 16 * g + 64 * c + 8 * h);
+                if (!has) {
+                    w = u32x4{0u, 0u, 0u, 0u};
+                }
+                qop[2 * c + h] = __builtin_bit_cast(bf16x8, w);
+            }
+        }
+    }
+
+    f32x4 oacc[T::kOMfma];
+#pragma unroll
+    for (int c = 0; c < T::kOMfma; ++c) {
+        oacc[c] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+    float m_run = -INFINITY;
+    float l_run = 0.0f;
+
+    TileRaw<D> cur, nxt;
+    int        t = wave;
+    if (t < n_tiles) {
+        load_tile<D>(cur, k, v, ks, vs, k0 + t * kTileKeys, k1, kvh, hkv, lane);
+    }
+    for (; t < n_tiles; t += kDecWaves) {
+        const int kb = k0 + t * kTileKeys;
+        if (t + kDecWaves < n_tiles) {
+            load_tile<D>(nxt, k, v, ks, vs, kb + kDecWaves * kTileKeys, k1, kvh, hkv, lane);
+        }
+
+        // Per-key factors: [0,32) = k_scale * scale * log2(e), [32,64) = v_scale.
+        sm_sc[wave][lane] = (lane < 32) ? cur.sc * scale_log2 : cur.sc;
+        __builtin_amdgcn_wave_barrier();
+
+        // S^T = K Q^T, two 16-key halves.
+        f32x4 s[2];
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            s[u] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int c = 0; c < T::kKChunks; ++c) {
+                bf16x8 a0, a1;
+                e4m3x16_to_bf16x8x2(cur.kraw[u][c], a0, a1);
+                s[u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, qop[2 * c], s[u], 0, 0, 0);
+                s[u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, qop[2 * c + 1], s[u], 0, 0, 0);
+            }
+        }
+
+        const f32x4 kf0 = *reinterpret_cast<const f32x4*>(&sm_sc[wave][4 * g]);
+        const f32x4 kf1 = *reinterpret_cast<const f32x4*>(&sm_sc[wave][16 + 4 * g]);
+        const f32x4 vf0 = *reinterpret_cast<const f32x4*>(&sm_sc[wave][32 + 4 * g]);
+        const f32x4 vf1 = *reinterpret_cast<const f32x4*>(&sm_sc[wave][48 + 4 * g]);
+
+        float x[8];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            x[r]     = s[0][r] * kf0[r];
+            x[4 + r] = s[1][r] * kf1[r];
+        }
+        if (kb + kTileKeys > k1) {  // ragged last tile of the split
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                if (kb + key_of(g, j) >= k1) {
+                    x[j] = -INFINITY;
+                }
+            }
+        }
+        float tmax = x[0];
+#pragma unroll
+        for (int j = 1; j < 8; ++j) {
+            tmax = fmaxf(tmax, x[j]);
+        }
+        tmax = wave_xor_max(tmax, 16);
+        tmax = wave_xor_max(tmax, 32);
+
+        const float m_new = fmaxf(m_run, tmax);
+        const float alpha = exp2f(m_run - m_new);
+        float       p[8];
+        float       psum = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            p[j] = exp2f(x[j] - m_new);
+            psum += p[j];
+        }
+        l_run = l_run * alpha + psum;
+        m_run = m_new;
+        if (__any(alpha != 1.0f)) {
+#pragma unroll
+            for (int c = 0; c < T::kOMfma; ++c) {
+                oacc[c] *= alpha;
+            }
+        }
+
+        u32x4 pw;
+        pw.x = pack_bf16x2(p[0] * vf0[0], p[1] * vf0[1]);
+        pw.y = pack_bf16x2(p[2] * vf0[2], p[3] * vf0[3]);
+        pw.z = pack_bf16x2(p[4] * vf1[0], p[5] * vf1[1]);
+        pw.w = pack_bf16x2(p[6] * vf1[2], p[7] * vf1[3]);
+        const bf16x8 pop = __builtin_bit_cast(bf16x8, pw);
+
+        // V^T operands: dword pj[j][w] holds bf16 of d = 2w, 2w+1 of key j.
+        uint32_t pj[8][T::kVBytes / 2];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+#pragma unroll
+            for (int w = 0; w < T::kVWords; ++w) {
+                const u32x2 b = e4m3x4_to_bf16x4(cur.vraw[j][w]);
+                pj[j][2 * w]     = b.x;
+                pj[j][2 * w + 1] = b.y;
+            }
+        }
+#pragma unroll
+        for (int c = 0; c < T::kOMfma; ++c) {
+            const int      pi  = c >> 1;
+            const uint32_t sel = (c & 1) ? 0x07060302u : 0x05040100u;
+            u32x4          aw;
+            aw.x = __builtin_amdgcn_perm(pj[1][pi], pj[0][pi], sel);
+            aw.y = __builtin_amdgcn_perm(pj[3][pi], pj[2][pi], sel);
+            aw.z = __builtin_amdgcn_perm(pj[5][pi], pj[4][pi], sel);
+            aw.w = __builtin_amdgcn_perm(pj[7][pi], pj[6][pi], sel);
+            oacc[c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                __builtin_bit_cast(bf16x8, aw), pop, oacc[c], 0, 0, 0);
+        }
+        __builtin_amdgcn_wave_barrier();
+        cur = nxt;
+    }
+
+    // ---- merge the waves of this workgroup --------------------------------
+    l_run = wave_xor_sum(l_run, 16);
+    l_run = wave_xor_sum(l_run, 32);
+    if (g == 0) {
+        sm_m[wave][n] = m_run;
+        sm_l[wave][n] = l_run;
+    }
+    __syncthreads();
+    float wf = 0.0f;  // this lane's head: factor of this wave against the block max
+    if (n < G) {
+        float M = -INFINITY;
+#pragma unroll
+        for (int w = 0; w < kDecWaves; ++w) {
+            M = fmaxf(M, sm_m[w][n]);
+        }
+        wf = (m_run == -INFINITY) ? 0.0f : exp2f(m_run - M);
+#pragma unroll
+        for (int c = 0; c < T::kOMfma; ++c) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int d = T::kVBytes * (4 * g + r) + c;
+                sm_o[(wave * G + n) * D + d] = oacc[c][r] * wf;
+            }
+        }
+    }
+    __syncthreads();
+
+    const int64_t hs     = static_cast<int64_t>(hq) * num_splits;
+    const int64_t slot0  = (static_cast<int64_t>(kvh) * num_splits + si) * G;
+    float*        part_m = partial;
+    float*        part_l = partial + hs;
+    float*        part_o = partial + 2 * hs;
+    for (int e = tid; e < G * D; e += kDecThreads) {
+        const int h = e / D;
+        const int d = e - h * D;
+        float     a = 0.0f;
+#pragma unroll
+        for (int w = 0; w < kDecWaves; ++w) {
+            a += sm_o[(w * G + h) * D + d];
+        }
+        part_o[(slot0 + h) * D + d] = a;
+    }
+    if (tid < G) {
+        float M = -INFINITY;
+        for (int w = 0; w < kDecWaves; ++w) {
+            M = fmaxf(M, sm_m[w][tid]);
+        }
+        float L = 0.0f;
+        for (int w = 0; w < kDecWaves; ++w) {
+            const float mw = sm_m[w][tid];
+            L += (mw == -INFINITY) ? 0.0f : sm_l[w][tid] * exp2f(mw - M);
+        }
+        part_m[slot0 + tid] = M;
+        part_l[slot0 + tid] = L;
+    }
+
+    // ---- last arrival merges the splits of this kv head -------------------
+    int* counters = reinterpret_cast<int*>(partial + hs * (D + 2));
+    __threadfence();
+    __syncthreads();
+    if (tid == 0) {
+        const int prev = atomicAdd(&counters[kvh], 1);
+        sm_last        = (prev == n_eff - 1) ? 1 : 0;
+    }
+    __syncthreads();
+    if (!sm_last) {
+        return;
+    }
+    __threadfence();
+
+    const int64_t base = static_cast<int64_t>(kvh) * num_splits * G;
+    for (int e = tid; e < G * D; e += kDecThreads) {
+        const int h = e / D;
+        const int d = e - h * D;
+        float     M = -INFINITY;
+        for (int s = 0; s < n_eff; ++s) {
+            M = fmaxf(M, part_m[base + s * G + h]);
+        }
+        float acc = 0.0f, L = 0.0f;
+        for (int s = 0; s < n_eff; ++s) {
+            const float f = exp2f(part_m[base + s * G + h] - M);
+            L += f * part_l[base + s * G + h];
+            acc += f * part_o[(base + s * G + h) * D + d];
+        }
+        out[static_cast<int64_t>(kvh * G + h) * D + d] = f32_to_bf16_bits(acc / L);
+    }
+    if (tid == 0) {
+        counters[kvh] = 0;
+    }
+}
+
+__global__ void zero_ints_kernel(int* p, int n) {
+    const int i = static_cast<int>(blockIdx.x * blockDim.x + threadIdx.x);
+    if (i < n) {
+        p[i] = 0;
+    }
+}
+
+__global__ void advance_position_kernel(int* pos, int delta) {
+    if (threadIdx.x == 0 && blockIdx.x == 0) {
+        *pos += delta;
+    }
+}
+
+template <int D>
+hipError_t launch_decode(uint16_t* out, const uint16_t* q, const uint8_t* k,
+                         const uint8_t* v, const float* ks, const float* vs,
+                         float* partial, int num_splits, const int* cache_len,
+                         int hq, int hkv, float scale, hipStream_t stream) {
+    const dim3 grid(static_cast<unsigned>(num_splits * hkv));
+    hipLaunchKernelGGL(flash_decode_kernel<D>, grid, dim3(kDecThreads), 0, stream,
+                       out, q, k, v, ks, vs, partial, num_splits, cache_len, hq,
+                       hkv, scale * kLog2e);
+    return hipGetLastError();
+}
+
+}  // namespace
+
+std::size_t decode_scratch_floats(int num_q_heads, int head_dim, int max_splits) {
+    const std::size_t hs = static_cast<std::size_t>(num_q_heads) *
+                           static_cast<std::size_t>(max_splits);
+    const std::size_t counters = (static_cast<std::size_t>(num_q_heads) + 63) / 64 * 64;
+    return hs * (static_cast<std::size_t>(head_dim) + 2) + counters;
+}
+
+hipError_t decode_scratch_reset_launch(float* partial, int num_q_heads,
+                                       int head_dim, int max_splits,
+                                       hipStream_t stream) {
+    const std::size_t hs = static_cast<std::size_t>(num_q_heads) *
+                           static_cast<std::size_t>(max_splits);
+    int* counters = reinterpret_cast<int*>(partial + hs * (head_dim + 2));
+    hipLaunchKernelGGL(zero_ints_kernel, dim3((num_q_heads + 255) / 256), dim3(256), 0,
+                       stream, counters, num_q_heads);
+    return hipGetLastError();
+}
+
+bool decode_mfma_supported(int num_q_heads, int num_kv_heads, int head_dim) {
+    const int G = num_q_heads / num_kv_heads;
+    return (head_dim == 64 || head_dim == 128 || head_dim == 256) && G <= 16 &&
+           G * head_dim <= kMaxGroupD;
+}
+
+hipError_t flash_decode_launch(uint16_t* out, const uint16_t* q,
+                               const uint8_t* k, const uint8_t* v,
+                               const float* k_scale, const float* v_scale,
+                               float* partial, int num_splits,
+                               const int* cache_len, int num_q_heads,
+                               int num_kv_heads, int head_dim, float scale,
+                               hipStream_t stream) {
+    switch (head_dim) {
+        case 64:
+            return launch_decode<64>(out, q, k, v, k_scale, v_scale, partial, num_splits,
+                                     cache_len, num_q_heads, num_kv_heads, scale, stream);
+        case 128:
+            return launch_decode<128>(out, q, k, v, k_scale, v_scale, partial, num_splits,
+                                      cache_len, num_q_heads, num_kv_heads, scale, stream);
+        case 256:
+            return launch_decode<256>(out, q, k, v, k_scale, v_scale, partial, num_splits,
+                                      cache_len, num_q_heads, num_kv_heads, scale, stream);
+        default:
+            return hipErrorInvalidValue;
+    }
+}
+
+hipError_t advance_position_launch(int* pos, int delta, hipStream_t stream) {
+    hipLaunchKernelGGL(advance_position_kernel, dim3(1), dim3(64), 0, stream, pos, delta);
+    return hipGetLastError();
+}
+
+}  // namespace rth

@@ -1,0 +1,60 @@
+// Internal launch functions behind the C ABI (capi.cpp). Each validates
+// nothing: argument checks live in the C ABI layer, these only pick a kernel
+// specialisation and enqueue it on `stream`.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+
+namespace rth {
+
+hipError_t quantize_kv_fp8_launch(uint8_t* q, float* scale, const uint16_t* x,
+                                  const int* at_pos, int rows_per_pos,
+                                  int num_rows, int head_dim, hipStream_t stream);
+
+hipError_t quantize_kv_fp8_scaled_launch(uint8_t* q, const float* scale,
+                                         const uint16_t* x, const int* at_pos,
+                                         int rows_per_pos, int num_rows,
+                                         int head_dim, hipStream_t stream);
+
+hipError_t kv_append_fp8_launch(uint8_t* k_q, uint8_t* v_q, float* k_scale,
+                                float* v_scale, const uint16_t* k,
+                                const uint16_t* v, const int* at_pos,
+                                int rows_per_pos, int num_rows, int head_dim,
+                                hipStream_t stream);
+
+// Split-K decode scratch: per (kv head, split) partial softmax state followed
+// by one arrival counter per kv head. Sized in floats.
+std::size_t decode_scratch_floats(int num_q_heads, int head_dim, int max_splits);
+
+hipError_t decode_scratch_reset_launch(float* partial, int num_q_heads,
+                                       int head_dim, int max_splits,
+                                       hipStream_t stream);
+
+hipError_t flash_decode_launch(uint16_t* out, const uint16_t* q,
+                               const uint8_t* k, const uint8_t* v,
+                               const float* k_scale, const float* v_scale,
+                               float* partial, int num_splits,
+                               const int* cache_len, int num_q_heads,
+                               int num_kv_heads, int head_dim, float scale,
+                               hipStream_t stream);
+
+hipError_t flash_prefill_launch(uint16_t* out, const uint16_t* q,
+                                const uint8_t* k, const uint8_t* v,
+                                const float* k_scale, const float* v_scale,
+                                int n_new, const int* cache_len,
+                                int num_q_heads, int num_kv_heads,
+                                int head_dim, float scale, hipStream_t stream);
+
+hipError_t attention_naive_launch(uint16_t* out, const uint16_t* q,
+                                  const uint8_t* k, const uint8_t* v,
+                                  const float* k_scale, const float* v_scale,
+                                  int n_new, const int* cache_len,
+                                  int num_q_heads, int num_kv_heads,
+                                  int head_dim, float scale, hipStream_t stream);
+
+hipError_t advance_position_launch(int* pos, int delta, hipStream_t stream);
+
+}  // namespace rth

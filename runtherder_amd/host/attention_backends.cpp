@@ -1,0 +1,81 @@
+// AdaptiveAttention, NaiveAttention and the backend factory over the C ABI
+// (reference src/attention/adaptive.cu, naive.cu, factory.cu).
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <memory>
+
+#include <rth_attn.h>
+#include <runtherder/attention/adaptive.h>
+#include <runtherder/attention/factory.h>
+#include <runtherder/attention/naive.h>
+#include <runtherder/check.h>
+#include <runtherder/device/check.h>
+
+namespace runtherder::attention {
+
+namespace {
+
+int device_num_splits(int num_kv_heads) {
+    int dev = 0;
+    RUNTHERDER_HIP_CHECK(hipGetDevice(&dev));
+    return rth_default_num_splits(num_kv_heads, dev);
+}
+
+}  // namespace
+
+AdaptiveAttention::AdaptiveAttention(const AttnConfig& config)
+    : AdaptiveAttention(config, device_num_splits(config.num_kv_heads)) {}
+
+AdaptiveAttention::AdaptiveAttention(const AttnConfig& config, int num_splits)
+    : config_(config), num_splits_(num_splits) {
+    RUNTHERDER_CHECK(num_splits >= 1, "AdaptiveAttention num_splits must be >= 1");
+    partial_ = device::make_device_unique<float>(
+        rth_split_scratch_floats(config.num_q_heads, config.head_dim, num_splits));
+    // The decode kernel's arrival counters start at zero and are left at zero.
+    RUNTHERDER_RTH_CHECK(rth_split_scratch_init(partial_.get(), config.num_q_heads,
+                                                config.head_dim, num_splits, nullptr));
+    RUNTHERDER_HIP_CHECK(hipDeviceSynchronize());
+}
+
+void AdaptiveAttention::run(__hip_bfloat16* out, const __hip_bfloat16* q, const KVView& kv,
+                            int n_new, const int* cache_len, hipStream_t stream) {
+    auto* o  = reinterpret_cast<std::uint16_t*>(out);
+    auto* qq = reinterpret_cast<const std::uint16_t*>(q);
+    auto* k  = reinterpret_cast<const std::uint8_t*>(kv.k);
+    auto* v  = reinterpret_cast<const std::uint8_t*>(kv.v);
+    if (n_new == 1) {
+        RUNTHERDER_RTH_CHECK(rth_attn_decode_split(o, qq, k, v, kv.k_scale, kv.v_scale,
+                                                   partial_.get(), num_splits_, cache_len,
+                                                   config_.num_q_heads, config_.num_kv_heads,
+                                                   config_.head_dim, config_.scale, stream));
+        return;
+    }
+    RUNTHERDER_RTH_CHECK(rth_attn_prefill(o, qq, k, v, kv.k_scale, kv.v_scale, n_new, cache_len,
+                                          config_.num_q_heads, config_.num_kv_heads,
+                                          config_.head_dim, config_.scale, stream));
+}
+
+NaiveAttention::NaiveAttention(const AttnConfig& config) noexcept : config_(config) {}
+
+void NaiveAttention::run(__hip_bfloat16* out, const __hip_bfloat16* q, const KVView& kv,
+                         int n_new, const int* cache_len, hipStream_t stream) {
+    RUNTHERDER_RTH_CHECK(rth_attn_naive(
+        reinterpret_cast<std::uint16_t*>(out), reinterpret_cast<const std::uint16_t*>(q),
+        reinterpret_cast<const std::uint8_t*>(kv.k), reinterpret_cast<const std::uint8_t*>(kv.v),
+        kv.k_scale, kv.v_scale, n_new, cache_len, config_.num_q_heads, config_.num_kv_heads,
+        config_.head_dim, config_.scale, stream));
+}
+
+std::unique_ptr<AttentionBackend> make_attention_backend(BackendKind kind,
+                                                         const AttnConfig& config) {
+    switch (kind) {
+        case BackendKind::Naive:
+            return std::make_unique<NaiveAttention>(config);
+        case BackendKind::Adaptive:
+            return std::make_unique<AdaptiveAttention>(config);
+    }
+    RUNTHERDER_CHECK(false, "unknown attention BackendKind");
+}
+
+}  // namespace runtherder::attention

@@ -1,0 +1,237 @@
+"""Torch-tensor front end of the C ABI, mirroring the reference's kernel free
+functions and its AttentionBackend / KVCache interface (reference
+include/runtherder/kernels/*.cuh, include/runtherder/attention/*.h,
+include/runtherder/engine/kv_cache.h). Same names, argument order and
+meaning; errors raise RthError instead of exiting the process.
+
+torch only provides device memory and the current stream here: every
+computation runs in libruntherder_attn.so.
+
+dtypes: bf16 tensors are torch.bfloat16, E4M3 cache bytes torch.uint8, scales
+torch.float32, device-resident positions torch.int32 (one element).
+"""
+from __future__ import annotations
+
+import enum
+import math
+from dataclasses import dataclass
+
+import torch
+
+from . import _ffi
+
+
+def _p(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def _stream(stream) -> int | None:
+    if stream is None:
+        return torch.cuda.current_stream().cuda_stream
+    if isinstance(stream, int):
+        return stream
+    return stream.cuda_stream
+
+
+def _need(t: torch.Tensor, dtype: torch.dtype, name: str) -> None:
+    if t.dtype != dtype:
+        raise TypeError(f"{name} must be {dtype}, got {t.dtype}")
+    if not t.is_cuda:
+        raise TypeError(f"{name} must be a device tensor")
+    if not t.is_contiguous():
+        raise TypeError(f"{name} must be contiguous")
+
+
+# ---- kernels ---------------------------------------------------------------
+
+def quantize_kv_fp8(q, scale, x, at_pos, rows_per_pos, num_rows, head_dim, stream=None):
+    """reference include/runtherder/kernels/quantization.cuh:50-57"""
+    _need(q, torch.uint8, "q"); _need(scale, torch.float32, "scale")
+    _need(x, torch.bfloat16, "x"); _need(at_pos, torch.int32, "at_pos")
+    _ffi.call("rth_kv_quantize_fp8", _p(q), _p(scale), _p(x), _p(at_pos),
+              rows_per_pos, num_rows, head_dim, _stream(stream))
+
+
+def quantize_kv_fp8_scaled(q, scale, x, at_pos, rows_per_pos, num_rows, head_dim, stream=None):
+    """Given-scale variant: scale[dst] is an input (no reference counterpart)."""
+    _need(q, torch.uint8, "q"); _need(scale, torch.float32, "scale")
+    _need(x, torch.bfloat16, "x"); _need(at_pos, torch.int32, "at_pos")
+    _ffi.call("rth_kv_quantize_fp8_scaled", _p(q), _p(scale), _p(x), _p(at_pos),
+              rows_per_pos, num_rows, head_dim, _stream(stream))
+
+
+def flash_split_scratch_floats(num_q_heads: int, head_dim: int, max_splits: int) -> int:
+    """reference include/runtherder/kernels/flash_decode.cuh:16-24 (+ counters)"""
+    return int(_ffi.load().rth_split_scratch_floats(num_q_heads, head_dim, max_splits))
+
+
+def new_flash_split_scratch(num_q_heads, head_dim, max_splits, device="cuda", stream=None):
+    """Allocates decode scratch and zeroes its arrival counters."""
+    n = flash_split_scratch_floats(num_q_heads, head_dim, max_splits)
+    t = torch.empty(n, dtype=torch.float32, device=device)
+    _ffi.call("rth_split_scratch_init", _p(t), num_q_heads, head_dim, max_splits,
+              _stream(stream))
+    return t
+
+
+def default_num_splits(num_kv_heads: int, device: int = 0) -> int:
+    return int(_ffi.load().rth_default_num_splits(num_kv_heads, device))
+
+
+def flash_decode_split_bf16(out, q, k, v, k_scale, v_scale, partial, num_splits, cache_len,
+                            num_q_heads, num_kv_heads, head_dim, scale, stream=None):
+    """reference include/runtherder/kernels/flash_decode.cuh:45-59"""
+    _need(out, torch.bfloat16, "out"); _need(q, torch.bfloat16, "q")
+    _need(k, torch.uint8, "k"); _need(v, torch.uint8, "v")
+    _need(k_scale, torch.float32, "k_scale"); _need(v_scale, torch.float32, "v_scale")
+    _need(partial, torch.float32, "partial"); _need(cache_len, torch.int32, "cache_len")
+    _ffi.call("rth_attn_decode_split", _p(out), _p(q), _p(k), _p(v), _p(k_scale),
+              _p(v_scale), _p(partial), num_splits, _p(cache_len), num_q_heads,
+              num_kv_heads, head_dim, float(scale), _stream(stream))
+
+
+def flash_prefill_bf16(out, q, k, v, k_scale, v_scale, n_new, cache_len, num_q_heads,
+                       num_kv_heads, head_dim, scale, stream=None):
+    """reference include/runtherder/kernels/flash_prefill.cuh:26-39"""
+    _need(out, torch.bfloat16, "out"); _need(q, torch.bfloat16, "q")
+    _need(k, torch.uint8, "k"); _need(v, torch.uint8, "v")
+    _need(k_scale, torch.float32, "k_scale"); _need(v_scale, torch.float32, "v_scale")
+    _need(cache_len, torch.int32, "cache_len")
+    _ffi.call("rth_attn_prefill", _p(out), _p(q), _p(k), _p(v), _p(k_scale), _p(v_scale),
+              n_new, _p(cache_len), num_q_heads, num_kv_heads, head_dim, float(scale),
+              _stream(stream))
+
+
+def attention_causal_bf16(out, q, k, v, k_scale, v_scale, n_new, cache_len, num_q_heads,
+                          num_kv_heads, head_dim, scale, stream=None):
+    """reference include/runtherder/kernels/attention.cuh:21-34"""
+    _need(out, torch.bfloat16, "out"); _need(q, torch.bfloat16, "q")
+    _need(k, torch.uint8, "k"); _need(v, torch.uint8, "v")
+    _need(k_scale, torch.float32, "k_scale"); _need(v_scale, torch.float32, "v_scale")
+    _need(cache_len, torch.int32, "cache_len")
+    _ffi.call("rth_attn_naive", _p(out), _p(q), _p(k), _p(v), _p(k_scale), _p(v_scale),
+              n_new, _p(cache_len), num_q_heads, num_kv_heads, head_dim, float(scale),
+              _stream(stream))
+
+
+def advance_position(pos, delta=1, stream=None):
+    """*pos += delta on device (lets one graph hold several decode steps)."""
+    _need(pos, torch.int32, "pos")
+    _ffi.call("rth_advance_position", _p(pos), int(delta), _stream(stream))
+
+
+# ---- interface -------------------------------------------------------------
+
+@dataclass(frozen=True)
+class AttnConfig:
+    """reference include/runtherder/attention/backend.h:14-19"""
+    num_q_heads: int
+    num_kv_heads: int
+    head_dim: int
+    scale: float
+
+    @staticmethod
+    def for_heads(num_q_heads, num_kv_heads, head_dim):
+        return AttnConfig(num_q_heads, num_kv_heads, head_dim, 1.0 / math.sqrt(head_dim))
+
+
+@dataclass(frozen=True)
+class KVView:
+    """reference include/runtherder/attention/kv_view.h:14-19"""
+    k: torch.Tensor
+    v: torch.Tensor
+    k_scale: torch.Tensor
+    v_scale: torch.Tensor
+
+
+class KVCache:
+    """reference include/runtherder/engine/kv_cache.h:23-104"""
+
+    def __init__(self, num_layers, max_seq_len, num_kv_heads, head_dim, device="cuda"):
+        for name, val in (("num_layers", num_layers), ("max_seq_len", max_seq_len),
+                          ("num_kv_heads", num_kv_heads), ("head_dim", head_dim)):
+            if val < 1:
+                raise ValueError(f"KVCache {name} must be >= 1")
+        self.num_layers, self._max_seq_len = num_layers, max_seq_len
+        self.num_kv_heads, self.head_dim = num_kv_heads, head_dim
+        shape = (num_layers, max_seq_len, num_kv_heads, head_dim)
+        self.k = torch.empty(shape, dtype=torch.uint8, device=device)
+        self.v = torch.empty(shape, dtype=torch.uint8, device=device)
+        self.k_scale = torch.empty(shape[:3], dtype=torch.float32, device=device)
+        self.v_scale = torch.empty(shape[:3], dtype=torch.float32, device=device)
+
+    def append(self, layer, k, v, n_new, at_pos, stream=None):
+        if not 0 <= layer < self.num_layers:
+            raise ValueError("KVCache append layer out of range")
+        if n_new < 1:
+            raise ValueError("KVCache append n_new must be >= 1")
+        _need(k, torch.bfloat16, "k"); _need(v, torch.bfloat16, "v")
+        _need(at_pos, torch.int32, "at_pos")
+        _ffi.call("rth_kv_append_fp8", _p(self.k[layer]), _p(self.v[layer]),
+                  _p(self.k_scale[layer]), _p(self.v_scale[layer]), _p(k), _p(v),
+                  _p(at_pos), n_new, self.num_kv_heads, self.head_dim, _stream(stream))
+
+    def view(self, layer) -> KVView:
+        if not 0 <= layer < self.num_layers:
+            raise ValueError("KVCache view layer out of range")
+        return KVView(self.k[layer], self.v[layer], self.k_scale[layer], self.v_scale[layer])
+
+    def max_seq_len(self) -> int:
+        return self._max_seq_len
+
+
+class AttentionBackend:
+    """reference include/runtherder/attention/backend.h:24-53"""
+
+    def run(self, out, q, kv: KVView, n_new, cache_len, stream=None):
+        raise NotImplementedError
+
+
+class AdaptiveAttention(AttentionBackend):
+    """reference src/attention/adaptive.cu: n_new == 1 -> split decode with
+    backend-owned scratch, else flash prefill. Split count defaults to the
+    device's (kv head, split) fill count."""
+
+    def __init__(self, config: AttnConfig, num_splits: int | None = None, device="cuda"):
+        self.config = config
+        self.num_splits = num_splits or default_num_splits(
+            config.num_kv_heads, torch.device(device).index or 0)
+        self.partial = new_flash_split_scratch(config.num_q_heads, config.head_dim,
+                                               self.num_splits, device=device)
+
+    def run(self, out, q, kv, n_new, cache_len, stream=None):
+        c = self.config
+        if n_new == 1:
+            flash_decode_split_bf16(out, q, kv.k, kv.v, kv.k_scale, kv.v_scale, self.partial,
+                                    self.num_splits, cache_len, c.num_q_heads, c.num_kv_heads,
+                                    c.head_dim, c.scale, stream)
+        else:
+            flash_prefill_bf16(out, q, kv.k, kv.v, kv.k_scale, kv.v_scale, n_new, cache_len,
+                               c.num_q_heads, c.num_kv_heads, c.head_dim, c.scale, stream)
+
+
+class NaiveAttention(AttentionBackend):
+    """reference src/attention/naive.cu"""
+
+    def __init__(self, config: AttnConfig):
+        self.config = config
+
+    def run(self, out, q, kv, n_new, cache_len, stream=None):
+        c = self.config
+        attention_causal_bf16(out, q, kv.k, kv.v, kv.k_scale, kv.v_scale, n_new, cache_len,
+                              c.num_q_heads, c.num_kv_heads, c.head_dim, c.scale, stream)
+
+
+class BackendKind(enum.Enum):
+    """reference include/runtherder/attention/factory.h:9-12"""
+    Naive = 0
+    Adaptive = 1
+
+
+def make_attention_backend(kind: BackendKind, config: AttnConfig) -> AttentionBackend:
+    """reference src/attention/factory.cu:11-21"""
+    if kind == BackendKind.Naive:
+        return NaiveAttention(config)
+    if kind == BackendKind.Adaptive:
+        return AdaptiveAttention(config)
+    raise ValueError("unknown attention BackendKind")

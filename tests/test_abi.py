@@ -1,0 +1,94 @@
+"""CPU checks of the boundary: the library loads, exports every symbol that
+include/*.h declares, rejects bad arguments before touching the GPU, and the
+C++ interface headers compile."""
+import ctypes
+import re
+import subprocess
+from pathlib import Path
+
+import pytest
+
+import runtherder_amd as R
+from runtherder_amd import _ffi
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "rth_attn.h"
+
+
+def declared_symbols():
+    text = HEADER.read_text()
+    return sorted(set(re.findall(r"\b(rth_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = ctypes.CDLL(str(_ffi.LIB_PATH))
+    names = declared_symbols()
+    assert len(names) >= 10
+    for name in names:
+        assert hasattr(lib, name), name
+    assert set(names) == set(_ffi.exported_symbols())
+
+
+def _err(name, *args):
+    with pytest.raises(_ffi.RthError) as e:
+        _ffi.call(name, *args)
+    return str(e.value)
+
+
+FAKE = 0x1000  # never dereferenced: every case fails its argument check first
+
+
+def test_prefill_rejects_head_dim():
+    msg = _err("rth_attn_prefill", FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 4, FAKE, 32, 8, 64,
+               ctypes.c_float(0.1), None)
+    assert "head_dim 128" in msg
+
+
+def test_decode_rejects_gqa_ratio_and_null():
+    assert "divisible" in _err("rth_attn_decode_split", FAKE, FAKE, FAKE, FAKE, FAKE, FAKE,
+                               FAKE, 4, FAKE, 30, 8, 128, ctypes.c_float(0.1), None)
+    assert "cache_len" in _err("rth_attn_decode_split", FAKE, FAKE, FAKE, FAKE, FAKE, FAKE,
+                               FAKE, 4, None, 32, 8, 128, ctypes.c_float(0.1), None)
+    assert "num_splits" in _err("rth_attn_decode_split", FAKE, FAKE, FAKE, FAKE, FAKE, FAKE,
+                                FAKE, 0, FAKE, 32, 8, 128, ctypes.c_float(0.1), None)
+    assert "head_dim" in _err("rth_attn_decode_split", FAKE, FAKE, FAKE, FAKE, FAKE, FAKE,
+                              FAKE, 4, FAKE, 32, 8, 96, ctypes.c_float(0.1), None)
+
+
+def test_quantize_rejects_bad_rows():
+    assert "divisible by 8" in _err("rth_kv_quantize_fp8", FAKE, FAKE, FAKE, FAKE, 1, 4, 12, None)
+    assert "at_pos" in _err("rth_kv_quantize_fp8", FAKE, FAKE, FAKE, None, 1, 4, 128, None)
+    assert "num_rows" in _err("rth_kv_quantize_fp8", FAKE, FAKE, FAKE, FAKE, 1, 0, 128, None)
+    assert "n_new" in _err("rth_kv_append_fp8", FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 0, 8,
+                           128, None)
+
+
+def test_naive_rejects_large_head_dim():
+    assert "512" in _err("rth_attn_naive", FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 1, FAKE, 8, 8,
+                         1024, ctypes.c_float(0.1), None)
+
+
+def test_scratch_size_formula():
+    # reference formula Hq*S*2 + Hq*S*D, plus counters rounded up to 64
+    assert R.flash_split_scratch_floats(32, 128, 64) == 32 * 64 * 2 + 32 * 64 * 128 + 64
+    assert R.flash_split_scratch_floats(24, 128, 32) == 24 * 32 * 130 + 64
+    assert _ffi.load().rth_split_scratch_floats(0, 128, 4) == 0
+
+
+def test_cpp_headers_compile():
+    src = """
+#include <runtherder/attention/factory.h>
+#include <runtherder/attention/adaptive.h>
+#include <runtherder/attention/naive.h>
+#include <runtherder/engine/kv_cache.h>
+#include <runtherder/kernels/quantization.h>
+#include <runtherder/kernels/flash_decode.h>
+#include <runtherder/kernels/flash_prefill.h>
+#include <runtherder/kernels/attention.h>
+static_assert(sizeof(runtherder::attention::KVView) == 4 * sizeof(void*));
+int main() { return 0; }
+"""
+    res = subprocess.run(["/opt/rocm/bin/hipcc", "-std=c++20", "-fsyntax-only", "-x", "hip",
+                          f"-I{ROOT / 'include'}", "--offload-arch=gfx950", "-"],
+                         input=src, capture_output=True, text=True)
+    assert res.returncode == 0, res.stderr[-3000:]

@@ -1,0 +1,141 @@
+"""Split-K flash decode on the GPU against the oracle (reference
+src/kernels/flash_decode.cu; cases of tests/kernels/test_flash_decode.cpp:
+148-170 plus the BASELINE configurations). Tolerance: max-abs 2e-2,
+mean-abs 2e-3 on bf16 outputs."""
+import numpy as np
+import pytest
+import torch
+
+import oracle_lib as O
+import runtherder_amd as R
+from gpu_util import (DEV, NTHREADS, bf16_dev, bf16_host, f32_dev, int_dev, step, sync,
+                      u8_dev)
+
+pytestmark = pytest.mark.gpu
+
+MAX_ABS, MEAN_ABS = 2e-2, 2e-3
+
+
+def make_cache(total, hkv, d, kind="mt", seed=0, per_head_scale=None):
+    if kind == "mt":
+        kx = O.mt19937_uniform_bf16((total * hkv, d), 1.0, 0xB0B)
+        vx = O.mt19937_uniform_bf16((total * hkv, d), 1.0, 0xCAFE)
+    else:
+        kx = O.normal_bf16((total * hkv, d), 1000 + seed)
+        vx = O.normal_bf16((total * hkv, d), 2000 + seed)
+    if per_head_scale is None:
+        k8, ks = O.quantize_kv_fp8(kx, d)
+        v8, vs = O.quantize_kv_fp8(vx, d)
+    else:
+        ks = np.tile(per_head_scale[0], total).astype(np.float32)
+        vs = np.tile(per_head_scale[1], total).astype(np.float32)
+        k8 = O.quantize_kv_fp8_scaled(kx, ks, d)
+        v8 = O.quantize_kv_fp8_scaled(vx, vs, d)
+    return kx, vx, k8, v8, ks, vs
+
+
+def gpu_decode(q, k8, v8, ks, vs, cache_len, hq, hkv, d, splits, scale):
+    step(f"decode ctx={cache_len + 1} hq={hq} hkv={hkv} d={d} splits={splits}")
+    out = torch.empty((hq, d), dtype=torch.bfloat16, device=DEV)
+    partial = R.new_flash_split_scratch(hq, d, splits)
+    R.flash_decode_split_bf16(out, bf16_dev(q), u8_dev(k8), u8_dev(v8), f32_dev(ks),
+                              f32_dev(vs), partial, splits, int_dev(cache_len), hq, hkv, d,
+                              scale)
+    sync()
+    return bf16_host(out)
+
+
+def check(got, q, k8, v8, ks, vs, cache_len, hq, hkv, d, scale):
+    want = O.attention_f32(q, k8, v8, ks, vs, 1, cache_len, hq, hkv, d, scale, NTHREADS)
+    mx, mean = O.bf16_err(got, want[0])
+    assert mx <= MAX_ABS and mean <= MEAN_ABS, (mx, mean)
+    return mx, mean
+
+
+@pytest.mark.parametrize("cache_len,hq,hkv,d,splits", [
+    (300, 32, 8, 128, 4), (0, 32, 8, 128, 1), (2, 8, 2, 64, 8), (1000, 32, 8, 128, 8),
+    (1000, 32, 8, 256, 8), (777, 16, 16, 64, 16), (99, 8, 1, 128, 3),
+    (40, 32, 8, 32, 4), (40, 8, 2, 512, 4), (130, 64, 4, 128, 8),
+])
+def test_reference_cases(cache_len, hq, hkv, d, splits):
+    scale = np.float32(1.0 / np.sqrt(d))
+    q = O.mt19937_uniform_bf16((hq, d), 1.0, 0xA11CE)
+    _, _, k8, v8, ks, vs = make_cache(cache_len + 1, hkv, d)
+    got = gpu_decode(q, k8, v8, ks, vs, cache_len, hq, hkv, d, splits, scale)
+    check(got, q, k8, v8, ks, vs, cache_len, hq, hkv, d, scale)
+
+
+@pytest.mark.parametrize("splits", [1, 2, 3, 8, 31, 32, 64, 100, 256])
+def test_split_count_sweep(splits):
+    hq, hkv, d, cache_len = 24, 8, 128, 2040
+    scale = np.float32(1.0 / np.sqrt(d))
+    q = O.normal_bf16((hq, d), 5)
+    _, _, k8, v8, ks, vs = make_cache(cache_len + 1, hkv, d, kind="normal", seed=1)
+    got = gpu_decode(q, k8, v8, ks, vs, cache_len, hq, hkv, d, splits, scale)
+    check(got, q, k8, v8, ks, vs, cache_len, hq, hkv, d, scale)
+
+
+def test_config1_per_tensor_scale():
+    """24Q/8KV, D 128, ctx 511; K/V N(0,1) quantized with one per-tensor
+    scale amax/448 broadcast into the per-(token, kv_head) slab."""
+    hq, hkv, d, ctx = 24, 8, 128, 511
+    scale = np.float32(1.0 / np.sqrt(d))
+    q = O.normal_bf16((hq, d), 11)
+    kx = O.normal_bf16((ctx * hkv, d), 12)
+    vx = O.normal_bf16((ctx * hkv, d), 13)
+    kt = np.float32(np.max(np.abs(O.bf16_to_f32(kx)))) / np.float32(448)
+    vt = np.float32(np.max(np.abs(O.bf16_to_f32(vx)))) / np.float32(448)
+    ks = np.full(ctx * hkv, kt, np.float32)
+    vs = np.full(ctx * hkv, vt, np.float32)
+    # the GPU given-scale quantizer must reproduce the oracle's bytes
+    step("config1 quantize_scaled")
+    k8d = torch.empty((ctx * hkv, d), dtype=torch.uint8, device=DEV)
+    v8d = torch.empty((ctx * hkv, d), dtype=torch.uint8, device=DEV)
+    R.quantize_kv_fp8_scaled(k8d, f32_dev(ks), bf16_dev(kx), int_dev(0), 1, ctx * hkv, d)
+    R.quantize_kv_fp8_scaled(v8d, f32_dev(vs), bf16_dev(vx), int_dev(0), 1, ctx * hkv, d)
+    sync()
+    k8 = O.quantize_kv_fp8_scaled(kx, ks, d)
+    v8 = O.quantize_kv_fp8_scaled(vx, vs, d)
+    assert np.array_equal(k8d.cpu().numpy(), k8) and np.array_equal(v8d.cpu().numpy(), v8)
+    got = gpu_decode(q, k8, v8, ks, vs, ctx - 1, hq, hkv, d, 32, scale)
+    check(got, q, k8, v8, ks, vs, ctx - 1, hq, hkv, d, scale)
+
+
+@pytest.mark.parametrize("ctx", [35, 2041, 8196, 32768])
+def test_config3_depths_single_layer(ctx):
+    hq, hkv, d = 24, 8, 128
+    scale = np.float32(1.0 / np.sqrt(d))
+    q = O.normal_bf16((hq, d), 21)
+    _, _, k8, v8, ks, vs = make_cache(ctx, hkv, d, kind="normal", seed=ctx)
+    got = gpu_decode(q, k8, v8, ks, vs, ctx - 1, hq, hkv, d, R.default_num_splits(hkv), scale)
+    check(got, q, k8, v8, ks, vs, ctx - 1, hq, hkv, d, scale)
+
+
+def test_config5_long_context_per_head_scales():
+    """32Q/8KV, ctx 131072, 64 splits, per-head scales ~U(0.01, 0.1)."""
+    hq, hkv, d, ctx = 32, 8, 128, 131072
+    scale = np.float32(1.0 / np.sqrt(d))
+    q = O.normal_bf16((hq, d), 51)
+    ph = (O.uniform_f32(hkv, 0.01, 0.1, 52), O.uniform_f32(hkv, 0.01, 0.1, 53))
+    _, _, k8, v8, ks, vs = make_cache(ctx, hkv, d, kind="normal", seed=5, per_head_scale=ph)
+    got = gpu_decode(q, k8, v8, ks, vs, ctx - 1, hq, hkv, d, 64, scale)
+    check(got, q, k8, v8, ks, vs, ctx - 1, hq, hkv, d, scale)
+
+
+def test_repeated_calls_rearm_counters():
+    """The fused merge re-arms its counters: back-to-back calls with
+    different depths on one scratch stay correct."""
+    hq, hkv, d = 32, 8, 128
+    scale = np.float32(1.0 / np.sqrt(d))
+    total = 3000
+    q = O.normal_bf16((hq, d), 61)
+    _, _, k8, v8, ks, vs = make_cache(total, hkv, d, kind="normal", seed=6)
+    partial = R.new_flash_split_scratch(hq, d, 32)
+    k8d, v8d, ksd, vsd, qd = u8_dev(k8), u8_dev(v8), f32_dev(ks), f32_dev(vs), bf16_dev(q)
+    for cl in (2999, 5, 1500, 0, 2999):
+        step(f"decode repeated cache_len={cl}")
+        out = torch.empty((hq, d), dtype=torch.bfloat16, device=DEV)
+        R.flash_decode_split_bf16(out, qd, k8d, v8d, ksd, vsd, partial, 32, int_dev(cl),
+                                  hq, hkv, d, scale)
+        sync()
+        check(bf16_host(out), q, k8, v8, ks, vs, cl, hq, hkv, d, scale)

@@ -1,0 +1,184 @@
+"""Causal flash prefill on the GPU against the oracle (reference
+src/kernels/flash_prefill.cu; cases of tests/kernels/test_flash_prefill.cpp:
+141-169 plus the BASELINE configurations). Tolerance: max-abs 2e-2,
+mean-abs 2e-3 on bf16 outputs."""
+import numpy as np
+import pytest
+import torch
+
+import oracle_lib as O
+import runtherder_amd as R
+from gpu_util import DEV, NTHREADS, bf16_dev, bf16_host, f32_dev, host, int_dev, step, sync, u8_dev
+
+pytestmark = pytest.mark.gpu
+
+MAX_ABS, MEAN_ABS = 2e-2, 2e-3
+
+
+def gpu_prefill(q, k8, v8, ks, vs, n_new, clen, hq, hkv, d, scale, naive=False):
+    step(f"{'naive' if naive else 'prefill'} n_new={n_new} clen={clen} hq={hq} hkv={hkv}")
+    out = torch.empty((n_new, hq, d), dtype=torch.bfloat16, device=DEV)
+    fn = R.attention_causal_bf16 if naive else R.flash_prefill_bf16
+    fn(out, bf16_dev(q), u8_dev(k8), u8_dev(v8), f32_dev(ks), f32_dev(vs), n_new,
+       int_dev(clen), hq, hkv, d, scale)
+    sync()
+    return bf16_host(out)
+
+
+def ref_inputs(n_new, clen, hq, hkv, d):
+    total = clen + n_new
+    q = O.mt19937_uniform_bf16((n_new, hq, d), 1.0, 0xA11CE)
+    k8, ks = O.quantize_kv_fp8(O.mt19937_uniform_bf16((total * hkv, d), 1.0, 0xB0B), d)
+    v8, vs = O.quantize_kv_fp8(O.mt19937_uniform_bf16((total * hkv, d), 1.0, 0xCAFE), d)
+    return q, k8, v8, ks, vs
+
+
+@pytest.mark.parametrize("naive", [False, True])
+@pytest.mark.parametrize("n_new,clen,hq,hkv", [
+    (16, 0, 32, 8), (20, 0, 32, 8), (8, 10, 32, 8), (64, 0, 24, 8), (3, 0, 8, 2),
+    (1, 0, 32, 8), (129, 0, 32, 8), (200, 77, 24, 8), (300, 1000, 8, 8), (257, 63, 16, 1),
+])
+def test_reference_cases(n_new, clen, hq, hkv, naive):
+    d = 128
+    scale = np.float32(1.0 / np.sqrt(d))
+    q, k8, v8, ks, vs = ref_inputs(n_new, clen, hq, hkv, d)
+    got = gpu_prefill(q, k8, v8, ks, vs, n_new, clen, hq, hkv, d, scale, naive)
+    want = O.attention_f32(q, k8, v8, ks, vs, n_new, clen, hq, hkv, d, scale, NTHREADS)
+    mx, mean = O.bf16_err(got, want)
+    assert mx <= MAX_ABS and mean <= MEAN_ABS, (mx, mean)
+
+
+def rope_qkv(n, hq, hkv, d, theta, llama3, seed):
+    q = O.normal_bf16((n, hq, d), seed)
+    k = O.normal_bf16((n, hkv, d), seed + 1)
+    v = O.normal_bf16((n, hkv, d), seed + 2)
+    inv = (O.rope_inv_freq_llama3(d, theta, 32.0, 1.0, 4.0, 8192) if llama3
+           else O.rope_inv_freq_plain(d, theta))
+    pos = np.arange(n, dtype=np.int32)
+    return O.rope_apply_bf16(q, pos, inv), O.rope_apply_bf16(k, pos, inv), v
+
+
+def append_and_check(cache_len, k, v, hkv, d, max_seq):
+    """Appends through the fused GPU kernel and checks the bytes bit-exactly."""
+    n = k.shape[0]
+    cache = R.KVCache(1, max_seq, hkv, d)
+    step(f"append n={n} at={cache_len}")
+    cache.append(0, bf16_dev(k), bf16_dev(v), n, int_dev(cache_len))
+    sync()
+    view = cache.view(0)
+    rows = slice(cache_len * hkv, (cache_len + n) * hkv)
+    wk, wks = O.quantize_kv_fp8(k, d)
+    wv, wvs = O.quantize_kv_fp8(v, d)
+    assert np.array_equal(host(view.k).reshape(-1, d)[rows], wk)
+    assert np.array_equal(host(view.v).reshape(-1, d)[rows], wv)
+    assert np.array_equal(host(view.k_scale).reshape(-1)[rows].view(np.uint32), wks.view(np.uint32))
+    assert np.array_equal(host(view.v_scale).reshape(-1)[rows].view(np.uint32), wvs.view(np.uint32))
+    return cache, view
+
+
+def test_config2_prefill_1021_rope_llama3():
+    """24Q/8KV, 1021 tokens, RoPE theta 5e5 with llama3 scaling (factor 32,
+    original context 8192); K/V through the append kernel; full oracle."""
+    n, hq, hkv, d = 1021, 24, 8, 128
+    scale = np.float32(1.0 / np.sqrt(d))
+    q, k, v = rope_qkv(n, hq, hkv, d, 5e5, True, 700)
+    cache, view = append_and_check(0, k, v, hkv, d, n)
+    out = torch.empty((n, hq, d), dtype=torch.bfloat16, device=DEV)
+    backend = R.make_attention_backend(R.BackendKind.Adaptive, R.AttnConfig.for_heads(hq, hkv, d))
+    step("config2 prefill")
+    backend.run(out, bf16_dev(q), view, n, int_dev(0))
+    sync()
+    k8, v8 = host(view.k).reshape(-1, d), host(view.v).reshape(-1, d)
+    ks, vs = host(view.k_scale).reshape(-1), host(view.v_scale).reshape(-1)
+    want = O.attention_f32(q, k8, v8, ks, vs, n, 0, hq, hkv, d, scale, NTHREADS)
+    mx, mean = O.bf16_err(bf16_host(out), want)
+    assert mx <= MAX_ABS and mean <= MEAN_ABS, (mx, mean)
+
+
+def sampled_rows(n, count, seed):
+    rng = np.random.default_rng(seed)
+    fixed = [0, 1, 63, 64, 127, 128, n // 2, n - 2, n - 1]
+    rows = set(r for r in fixed if 0 <= r < n) | set(rng.integers(0, n, count).tolist())
+    return sorted(rows)
+
+
+def check_rows(got, q, k8, v8, ks, vs, clen, rows, hq, hkv, d, scale):
+    worst = 0.0
+    for t in rows:
+        want = O.attention_f32(q[t:t + 1], k8, v8, ks, vs, 1, clen + t, hq, hkv, d, scale,
+                               NTHREADS)
+        mx, mean = O.bf16_err(got[t], want[0])
+        assert mx <= MAX_ABS and mean <= MEAN_ABS, (t, mx, mean)
+        worst = max(worst, mx)
+    return worst
+
+
+@pytest.mark.parametrize("n", [2048, 4096, 8192, 16384])
+def test_config4_prefill_sampled_rows(n):
+    """32Q/8KV, RoPE theta 1e6, FP8 writeback; oracle on sampled rows."""
+    hq, hkv, d = 32, 8, 128
+    scale = np.float32(1.0 / np.sqrt(d))
+    q, k, v = rope_qkv(n, hq, hkv, d, 1e6, False, 900 + n)
+    cache, view = append_and_check(0, k, v, hkv, d, n)
+    out = torch.empty((n, hq, d), dtype=torch.bfloat16, device=DEV)
+    step(f"config4 prefill n={n}")
+    R.flash_prefill_bf16(out, bf16_dev(q), view.k, view.v, view.k_scale, view.v_scale, n,
+                         int_dev(0), hq, hkv, d, scale)
+    sync()
+    k8, v8 = host(view.k).reshape(-1, d), host(view.v).reshape(-1, d)
+    ks, vs = host(view.k_scale).reshape(-1), host(view.v_scale).reshape(-1)
+    check_rows(bf16_host(out), q, k8, v8, ks, vs, 0, sampled_rows(n, 12, n), hq, hkv, d, scale)
+
+
+def test_chunked_prefill_equals_full_tail():
+    """Size-independent property: a chunked prefill (cache_len > 0) equals the
+    tail rows of one full prefill over the same cache."""
+    hq, hkv, d, total, clen = 32, 8, 128, 3000, 2237
+    scale = np.float32(1.0 / np.sqrt(d))
+    q, k, v = rope_qkv(total, hq, hkv, d, 1e6, False, 1234)
+    cache, view = append_and_check(0, k, v, hkv, d, total)
+    full = torch.empty((total, hq, d), dtype=torch.bfloat16, device=DEV)
+    tail = torch.empty((total - clen, hq, d), dtype=torch.bfloat16, device=DEV)
+    qd = bf16_dev(q)
+    step("prefill full vs chunk")
+    R.flash_prefill_bf16(full, qd, view.k, view.v, view.k_scale, view.v_scale, total,
+                         int_dev(0), hq, hkv, d, scale)
+    R.flash_prefill_bf16(tail, qd[clen:].contiguous(), view.k, view.v, view.k_scale,
+                         view.v_scale, total - clen, int_dev(clen), hq, hkv, d, scale)
+    sync()
+    mx, mean = O.bf16_err(bf16_host(full)[clen:], bf16_host(tail))
+    assert mx <= 1e-2 and mean <= 1e-3, (mx, mean)
+
+
+def test_config5_chunked_prefill_into_128k_cache():
+    """4096-token chunk appended at cache_len 126976 of a 131072 cache with
+    per-head given scales for the history; oracle on sampled rows."""
+    hq, hkv, d, S = 32, 8, 128, 131072
+    clen, n = 126976, 4096
+    scale = np.float32(1.0 / np.sqrt(d))
+    hist_k = O.normal_bf16((clen * hkv, d), 71)
+    hist_v = O.normal_bf16((clen * hkv, d), 72)
+    pks = np.tile(O.uniform_f32(hkv, 0.01, 0.1, 73), clen)
+    pvs = np.tile(O.uniform_f32(hkv, 0.01, 0.1, 74), clen)
+    cache = R.KVCache(1, S, hkv, d)
+    view = cache.view(0)
+    step("config5 history fill")
+    R.quantize_kv_fp8_scaled(view.k.view(-1, d)[: clen * hkv], f32_dev(pks), bf16_dev(hist_k),
+                             int_dev(0), 1, clen * hkv, d)
+    R.quantize_kv_fp8_scaled(view.v.view(-1, d)[: clen * hkv], f32_dev(pvs), bf16_dev(hist_v),
+                             int_dev(0), 1, clen * hkv, d)
+    view.k_scale.view(-1)[: clen * hkv].copy_(torch.from_numpy(pks))
+    view.v_scale.view(-1)[: clen * hkv].copy_(torch.from_numpy(pvs))
+    q, k, v = rope_qkv(n, hq, hkv, d, 1e6, False, 75)
+    step("config5 append chunk")
+    cache.append(0, bf16_dev(k), bf16_dev(v), n, int_dev(clen))
+    out = torch.empty((n, hq, d), dtype=torch.bfloat16, device=DEV)
+    step("config5 chunked prefill")
+    R.flash_prefill_bf16(out, bf16_dev(q), view.k, view.v, view.k_scale, view.v_scale, n,
+                         int_dev(clen), hq, hkv, d, scale)
+    sync()
+    k8, v8 = host(view.k).reshape(-1, d), host(view.v).reshape(-1, d)
+    ks, vs = host(view.k_scale).reshape(-1), host(view.v_scale).reshape(-1)
+    wk = O.quantize_kv_fp8_scaled(hist_k, pks, d)
+    assert np.array_equal(k8[: clen * hkv], wk)
+    check_rows(bf16_host(out), q, k8, v8, ks, vs, clen, sampled_rows(n, 4, 5), hq, hkv, d, scale)
