@@ -1,0 +1,346 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X attention hot path (one GPU).
+
+Headline: decode attention HBM GB/s at 8K context (a
+Llama-3.2-3B-shaped 28-layer decode, 24 Q / 8 KV heads, head_dim 128, FP8 E4M3
+KV cache prefilled with quantized N(0,1), one token per step: per layer the
+fused K/V append then the split-K flash decode, 128 steps captured in one HIP
+graph). A "step" is one decode token through all 28 layers. Secondary: causal
+prefill attention TFLOP/s at 4096 tokens (config 4: 32 Q / 8 KV heads, RoPE'd
+N(0,1) inputs, FP8 writeback).
+
+Algorithmic units (no credit for re-reads or scratch):
+  decode bytes / call  = ctx*Hkv*D*2 + ctx*Hkv*8 + Hq*D*4
+  prefill flops / call = 4*Hq*D*P, P = n*clen + n*(n+1)/2
+
+Prints one JSON line. Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+PEAK_HBM_GBS = 8000.0         # MI355X HBM3E, AMD published
+PEAK_BF16_TFLOPS = 2500.0     # MI355X dense bf16 MFMA, AMD published
+GRAPH_STEPS = 128
+
+
+def decode_bytes(ctx: int, hq: int, hkv: int, d: int) -> int:
+    return ctx * hkv * d * 2 + ctx * hkv * 8 + hq * d * 4
+
+
+def prefill_flops(n: int, clen: int, hq: int, d: int) -> int:
+    pairs = n * clen + n * (n + 1) // 2
+    return 4 * hq * d * pairs
+
+
+class EventTimer:
+    """HIP events on the stream the kernels run on."""
+
+    def __init__(self, torch, stream):
+        self.torch, self.stream = torch, stream
+        self.a = torch.cuda.Event(enable_timing=True)
+        self.b = torch.cuda.Event(enable_timing=True)
+
+    def __enter__(self):
+        self.a.record(self.stream)
+        return self
+
+    def __exit__(self, *exc):
+        self.b.record(self.stream)
+        self.b.synchronize()
+        self.ms = self.a.elapsed_time(self.b)
+
+
+def bench_decode(torch, R, args, stream):
+    hq, hkv, d, L = 24, 8, 128, 28
+    ctx0 = args.ctx                          # keys attended at the first step
+    depth = ctx0 - 1                         # history prefilled before step 0
+    max_seq = depth + GRAPH_STEPS + 1
+    scale = 1.0 / math.sqrt(d)
+    dev = torch.device("cuda:0")
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(1234)
+
+    cache = R.KVCache(L, max_seq, hkv, d, device=dev)
+    backend = R.AdaptiveAttention(R.AttnConfig(hq, hkv, d, scale))
+    pos = torch.zeros(1, dtype=torch.int32, device=dev)
+    chunk = 4096
+    with torch.cuda.stream(stream):
+        for l in range(L):
+            for s0 in range(0, depth, chunk):
+                n = min(chunk, depth - s0)
+                k = torch.randn((n, hkv, d), generator=gen, device=dev).to(torch.bfloat16)
+                v = torch.randn((n, hkv, d), generator=gen, device=dev).to(torch.bfloat16)
+                pos.fill_(s0)
+                cache.append(l, k, v, n, pos)
+        # per-step, per-layer new token: q, k, v (distinct per step and layer)
+        qs = torch.randn((GRAPH_STEPS, L, hq, d), generator=gen, device=dev).to(torch.bfloat16)
+        ks = torch.randn((GRAPH_STEPS, L, hkv, d), generator=gen, device=dev).to(torch.bfloat16)
+        vs = torch.randn((GRAPH_STEPS, L, hkv, d), generator=gen, device=dev).to(torch.bfloat16)
+        out = torch.empty((GRAPH_STEPS, L, hq, d), dtype=torch.bfloat16, device=dev)
+        pos.fill_(depth)
+    torch.cuda.synchronize()
+
+    def run_steps():
+        for s in range(GRAPH_STEPS):
+            for l in range(L):
+                cache.append(l, ks[s, l], vs[s, l], 1, pos)
+                backend.run(out[s, l], qs[s, l], cache.view(l), 1, pos)
+            R.advance_position(pos, 1)
+        R.advance_position(pos, -GRAPH_STEPS)   # replays are idempotent
+
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        run_steps()
+    torch.cuda.synchronize()
+
+    replays_w = max(1, math.ceil(args.warmup / GRAPH_STEPS))
+    replays = max(1, math.ceil(args.steps / GRAPH_STEPS))
+    with torch.cuda.stream(stream):
+        for _ in range(replays_w):
+            graph.replay()
+    torch.cuda.synchronize()
+    with torch.cuda.stream(stream):
+        with EventTimer(torch, stream) as t:
+            for _ in range(replays):
+                graph.replay()
+    torch.cuda.synchronize()
+    steps = replays * GRAPH_STEPS
+    ms_per_step = t.ms / steps
+    step_bytes = [sum(decode_bytes(ctx0 + s, hq, hkv, d) for _ in range(L))
+                  for s in range(GRAPH_STEPS)]
+    total_bytes = replays * sum(step_bytes)
+    value_gbs = total_bytes / (t.ms * 1e-3) / 1e9
+
+    # Dominant kernel alone: back-to-back decode launches rotating over the 28
+    # layers (defeats the 256 MB Infinity Cache), HIP events on its stream.
+    n_launch = L * 20
+    with torch.cuda.stream(stream):
+        pos.fill_(depth)
+        for l in range(L):
+            backend.run(out[0, l], qs[0, l], cache.view(l), 1, pos)
+        torch.cuda.synchronize()
+        with EventTimer(torch, stream) as tk:
+            for i in range(n_launch):
+                l = i % L
+                backend.run(out[0, l], qs[0, l], cache.view(l), 1, pos)
+    torch.cuda.synchronize()
+    kern_us = tk.ms * 1e3 / n_launch
+    kbytes = decode_bytes(depth + 1, hq, hkv, d)
+    achieved = kbytes / (kern_us * 1e-6) / 1e9
+    return {
+        "value": value_gbs, "ms_per_step": ms_per_step, "steps": steps,
+        "warmup": replays_w * GRAPH_STEPS, "ctx": ctx0, "splits": backend.num_splits,
+        "kernel_us": kern_us, "kernel_bytes": kbytes, "kernel_gbs": achieved,
+        "cache": cache, "qs": qs, "depth": depth, "hq": hq, "hkv": hkv, "d": d,
+        "scale": scale, "out": out, "backend": backend, "pos": pos,
+    }
+
+
+def bench_prefill(torch, R, stream, n=4096, iters=10):
+    hq, hkv, d = 32, 8, 128
+    scale = 1.0 / math.sqrt(d)
+    dev = torch.device("cuda:0")
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(4321)
+    cache = R.KVCache(1, n, hkv, d, device=dev)
+    pos = torch.zeros(1, dtype=torch.int32, device=dev)
+    with torch.cuda.stream(stream):
+        q = torch.randn((n, hq, d), generator=gen, device=dev).to(torch.bfloat16)
+        k = torch.randn((n, hkv, d), generator=gen, device=dev).to(torch.bfloat16)
+        v = torch.randn((n, hkv, d), generator=gen, device=dev).to(torch.bfloat16)
+        out = torch.empty((n, hq, d), dtype=torch.bfloat16, device=dev)
+        view = cache.view(0)
+        cache.append(0, k, v, n, pos)
+        for _ in range(3):
+            R.flash_prefill_bf16(out, q, view.k, view.v, view.k_scale, view.v_scale, n, pos,
+                                 hq, hkv, d, scale)
+        torch.cuda.synchronize()
+        with EventTimer(torch, stream) as t:
+            for _ in range(iters):
+                R.flash_prefill_bf16(out, q, view.k, view.v, view.k_scale, view.v_scale, n,
+                                     pos, hq, hkv, d, scale)
+        with EventTimer(torch, stream) as ta:
+            for _ in range(iters):
+                cache.append(0, k, v, n, pos)
+    torch.cuda.synchronize()
+    us = t.ms * 1e3 / iters
+    fl = prefill_flops(n, 0, hq, d)
+    tflops = fl / (us * 1e-6) / 1e12
+    app_us = ta.ms * 1e3 / iters
+    app_bytes = n * hkv * d * 4 + n * hkv * d * 2 + n * hkv * 8
+    return {"n": n, "us": us, "flops": fl, "tflops": tflops, "append_us": app_us,
+            "append_gbs": app_bytes / (app_us * 1e-6) / 1e9}
+
+
+def decode_kernel_sweep(torch, R, stream, points):
+    """Per-call decode time (split kernel + merge kernel) at several context
+    depths, rotating over enough layers that the working set exceeds the
+    256 MB Infinity Cache. points: (hq, hkv, ctx, splits or None)."""
+    res = []
+    d = 128
+    dev = torch.device("cuda:0")
+    for hq, hkv, ctx, splits in points:
+        per_layer = ctx * hkv * d * 2 + ctx * hkv * 8
+        L = max(2, min(28, math.ceil(600e6 / per_layer)))
+        cache = R.KVCache(L, ctx, hkv, d, device=dev)
+        cache.k.random_(0, 126)
+        cache.v.random_(0, 126)
+        cache.k_scale.uniform_(0.001, 0.01)
+        cache.v_scale.uniform_(0.001, 0.01)
+        backend = R.AdaptiveAttention(R.AttnConfig(hq, hkv, d, 1.0 / math.sqrt(d)),
+                                      num_splits=splits)
+        q = torch.randn((L, hq, d), device=dev).to(torch.bfloat16)
+        out = torch.empty((L, hq, d), dtype=torch.bfloat16, device=dev)
+        pos = torch.full((1,), ctx - 1, dtype=torch.int32, device=dev)
+        n = L * max(2, math.ceil(200 / L))
+        with torch.cuda.stream(stream):
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g, stream=stream):
+                for i in range(n):
+                    backend.run(out[i % L], q[i % L], cache.view(i % L), 1, pos)
+            g.replay()
+            torch.cuda.synchronize()
+            with EventTimer(torch, stream) as t:
+                g.replay()
+        torch.cuda.synchronize()
+        us = t.ms * 1e3 / n
+        nbytes = decode_bytes(ctx, hq, hkv, d)
+        res.append({"hq": hq, "hkv": hkv, "ctx": ctx, "splits": backend.num_splits,
+                    "layers": L, "us": round(us, 2), "gbs": round(nbytes / us / 1e3, 1),
+                    "frac": round(nbytes / us / 1e3 / PEAK_HBM_GBS, 4)})
+        print(json.dumps({"decode_sweep": res[-1]}), flush=True)
+        del cache, backend, q, out
+        torch.cuda.empty_cache()
+    return res
+
+
+def prefill_sweep(torch, R, stream, ns):
+    out = []
+    for n in ns:
+        pf = bench_prefill(torch, R, stream, n=n, iters=5 if n > 8192 else 10)
+        out.append({"n": n, "us": round(pf["us"], 1), "tflops": round(pf["tflops"], 1),
+                    "frac": round(pf["tflops"] / PEAK_BF16_TFLOPS, 4)})
+        print(json.dumps({"prefill_sweep": out[-1]}), flush=True)
+        torch.cuda.empty_cache()
+    return out
+
+
+def cpu_baseline(torch, dec, budget_s=12.0):
+    """Oracle (C restatement of the reference's naive fp32 attention,
+    reference src/kernels/attention.cu:34-91) on host threads, decode at the
+    same context over the same cache bytes; bounded sample of layers."""
+    sys.path.insert(0, str(ROOT / "tests"))
+    import numpy as np
+    import oracle_lib as O
+
+    cores = max(1, min(16, os.cpu_count() or 1))
+    hq, hkv, d, depth = dec["hq"], dec["hkv"], dec["d"], dec["depth"]
+    cache = dec["cache"]
+    layers, t_total, nbytes = 0, 0.0, 0
+    while t_total < budget_s and layers < 28:
+        view = cache.view(layers)
+        keys = depth + 1
+        k8 = view.k[:keys].cpu().numpy().reshape(-1, d)
+        v8 = view.v[:keys].cpu().numpy().reshape(-1, d)
+        ks = view.k_scale[:keys].cpu().numpy().reshape(-1)
+        vs = view.v_scale[:keys].cpu().numpy().reshape(-1)
+        q = dec["qs"][0, layers].view(torch.int16).cpu().numpy().view(np.uint16)
+        t0 = time.perf_counter()
+        O.attention_f32(q, k8, v8, ks, vs, 1, depth, hq, hkv, d, np.float32(dec["scale"]), cores)
+        t_total += time.perf_counter() - t0
+        nbytes += decode_bytes(keys, hq, hkv, d)
+        layers += 1
+    return {"value": nbytes / t_total / 1e9, "unit": "GB/s", "cores": cores, "kind": "port",
+            "sample": f"{layers} layer(s) of the 28-layer decode at ctx {depth + 1}, "
+                      f"fp32 two-pass naive attention over the same FP8 cache bytes, "
+                      f"{t_total:.1f} s"}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=512)
+    ap.add_argument("--warmup", type=int, default=128)
+    ap.add_argument("--ctx", type=int, default=8196)
+    ap.add_argument("--prefill-n", type=int, default=4096)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--sweep", action="store_true",
+                    help="per-call decode and prefill sweeps over the BASELINE depths")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py runs on one GPU only (the attention hot path is single-GPU); "
+              f"--gpus {args.gpus} is not supported", file=sys.stderr)
+        return 2
+
+    import torch
+    import runtherder_amd as R
+
+    R._ffi.load()
+    stream = torch.cuda.Stream()
+    torch.cuda.synchronize()
+    if args.sweep:
+        decode_kernel_sweep(torch, R, stream, [(24, 8, 35, None), (24, 8, 2041, None),
+                                               (24, 8, 8196, None), (24, 8, 32768, None),
+                                               (32, 8, 131072, 64)])
+        prefill_sweep(torch, R, stream, [1021, 2048, 4096, 8192, 16384])
+        return 0
+    dec = bench_decode(torch, R, args, stream)
+    pf = bench_prefill(torch, R, stream, n=args.prefill_n)
+    cpu = None if args.no_cpu else cpu_baseline(torch, dec)
+
+    line = {
+        "metric": "decode attn HBM GB/s (% peak) @8K ctx; prefill attn TFLOP/s @4K tok",
+        "value": round(dec["value"], 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": dec["steps"],
+        "warmup": dec["warmup"],
+        "ms_per_step": round(dec["ms_per_step"], 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "e4m3-kv/bf16-mfma/fp32-acc",
+        "data": "synthetic: N(0,1) bf16 q/k/v, k/v quantized to FP8 E4M3 by the append kernel",
+        "config": {
+            "workload": "config3: 28-layer Llama-3.2-3B-shaped decode attention, 24Q/8KV, "
+                        "head_dim 128, ctx 8196..8323, per layer append+split-K decode, "
+                        "128 steps per HIP graph",
+            "ctx": dec["ctx"], "layers": 28, "num_splits": dec["splits"],
+            "parallelism": "single GPU",
+        },
+        "percent_of_peak": round(100.0 * dec["value"] / PEAK_HBM_GBS, 2),
+        "roofline": {
+            "bound": "hbm", "achieved": round(dec["kernel_gbs"], 1), "peak": PEAK_HBM_GBS,
+            "unit": "GB/s", "frac": round(dec["kernel_gbs"] / PEAK_HBM_GBS, 4),
+            "traffic": None,
+            "kernel": "flash_decode_kernel<128>",
+            "kernel_us": round(dec["kernel_us"], 3), "bytes_per_launch": dec["kernel_bytes"],
+        },
+        "prefill": {
+            "metric": "prefill attn TFLOP/s @4K tok",
+            "workload": f"config4: 32Q/8KV head_dim 128 causal prefill, n={pf['n']}, clen 0",
+            "value": round(pf["tflops"], 1), "unit": "TFLOP/s", "us": round(pf["us"], 1),
+            "roofline": {"bound": "mfma", "achieved": round(pf["tflops"], 1),
+                         "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                         "frac": round(pf["tflops"] / PEAK_BF16_TFLOPS, 4),
+                         "flops_per_launch": pf["flops"]},
+            "append_us": round(pf["append_us"], 2), "append_gbs": round(pf["append_gbs"], 1),
+        },
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -66,15 +66,9 @@ int rth_kv_append_fp8(uint8_t* k_cache, uint8_t* v_cache, float* k_scale,
 
 /* Replaces kernels::flash_split_scratch_floats (reference
  * include/runtherder/kernels/flash_decode.cuh:16-24): floats of decode
- * scratch for max_splits splits. Layout: [Hq*S] m, [Hq*S] l, [Hq*S*D] acc as
- * in the reference, followed by one int arrival counter per kv head. */
+ * scratch for max_splits splits, Hq*S*2 + Hq*S*D, laid out as [Hq*S] m,
+ * [Hq*S] l, [Hq*S*D] acc like the reference's. No initialization needed. */
 size_t rth_split_scratch_floats(int num_q_heads, int head_dim, int max_splits);
-
-/* Zeroes the arrival counters of a decode scratch (once, after allocation;
- * rth_attn_decode_split leaves them zeroed after every call). No counterpart
- * in the reference, whose scratch needs no initialization. */
-int rth_split_scratch_init(float* partial, int num_q_heads, int head_dim,
-                           int max_splits, void* stream);
 
 /* Split count AdaptiveAttention uses on `device` for num_kv_heads kv heads:
  * enough (kv head, split) workgroups to fill every compute unit. */
@@ -83,10 +77,10 @@ int rth_default_num_splits(int num_kv_heads, int device);
 /* Replaces kernels::flash_decode_split_bf16 (reference
  * include/runtherder/kernels/flash_decode.cuh:45-59): one query token,
  * attends *cache_len + 1 keys, split-K over num_splits key ranges with a
- * log-sum-exp merge. `partial` is caller-owned scratch of
- * rth_split_scratch_floats(Hq, D, num_splits) floats whose counters were
- * zeroed once by rth_split_scratch_init. head_dim in {32,64,128,256,512};
- * 64/128/256 with Hq/Hkv <= 16 run the MFMA kernel, the rest the naive one. */
+ * log-sum-exp merge (two kernels: splits, then merge). `partial` is
+ * caller-owned scratch of rth_split_scratch_floats(Hq, D, num_splits) floats.
+ * head_dim in {32,64,128,256,512}; 64/128/256 with Hq/Hkv <= 16 run the MFMA
+ * kernel, the rest the naive one. */
 int rth_attn_decode_split(uint16_t* out, const uint16_t* q, const uint8_t* k,
                           const uint8_t* v, const float* k_scale,
                           const float* v_scale, float* partial, int num_splits,

@@ -27,7 +27,7 @@ public:
 private:
     AttnConfig                     config_;
     int                            num_splits_;
-    device::DeviceUniquePtr<float> partial_;  // split decode scratch + counters
+    device::DeviceUniquePtr<float> partial_;  // split decode reduction scratch
 };
 
 }  // namespace runtherder::attention

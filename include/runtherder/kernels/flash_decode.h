@@ -14,18 +14,11 @@
 
 namespace runtherder::kernels {
 
-// Floats of decode scratch for max_splits splits: the reference's m, l, acc
-// slab followed by one arrival counter per kv head. Zero the counters once
-// with init_flash_split_scratch after allocating.
+// Floats of decode scratch for max_splits splits: [Hq, S] m, then l, then
+// [Hq, S, D] acc, one contiguous slab (same formula as the reference).
 [[nodiscard]] inline std::size_t flash_split_scratch_floats(int num_q_heads, int head_dim,
                                                             int max_splits) {
     return rth_split_scratch_floats(num_q_heads, head_dim, max_splits);
-}
-
-inline void init_flash_split_scratch(float* partial, int num_q_heads, int head_dim,
-                                     int max_splits, hipStream_t stream = nullptr) {
-    RUNTHERDER_RTH_CHECK(
-        rth_split_scratch_init(partial, num_q_heads, head_dim, max_splits, stream));
 }
 
 // One query token attends *cache_len + 1 keys in num_splits key ranges merged by

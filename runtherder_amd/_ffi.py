@@ -20,7 +20,6 @@ _SIGNATURES = {
     "rth_kv_quantize_fp8_scaled": (_c_int, [_vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, _vp]),
     "rth_kv_append_fp8": (_c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, _vp]),
     "rth_split_scratch_floats": (ctypes.c_size_t, [_c_int, _c_int, _c_int]),
-    "rth_split_scratch_init": (_c_int, [_vp, _c_int, _c_int, _c_int, _vp]),
     "rth_default_num_splits": (_c_int, [_c_int, _c_int]),
     "rth_attn_decode_split": (_c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_int, _vp,
                                        _c_int, _c_int, _c_int, ctypes.c_float, _vp]),

@@ -129,16 +129,6 @@ size_t rth_split_scratch_floats(int num_q_heads, int head_dim, int max_splits) {
     return rth::decode_scratch_floats(num_q_heads, head_dim, max_splits);
 }
 
-int rth_split_scratch_init(float* partial, int num_q_heads, int head_dim,
-                           int max_splits, void* stream) {
-    RTH_REQUIRE(partial != nullptr, "partial must not be null");
-    RTH_REQUIRE(num_q_heads >= 1 && head_dim >= 1 && max_splits >= 1,
-                "num_q_heads, head_dim and max_splits must be >= 1");
-    return check_hip(rth::decode_scratch_reset_launch(partial, num_q_heads, head_dim,
-                                                      max_splits, as_stream(stream)),
-                     "rth_split_scratch_init");
-}
-
 int rth_default_num_splits(int num_kv_heads, int device) {
     int cus = 0;
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) !=

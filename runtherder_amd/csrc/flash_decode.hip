@@ -18,15 +18,17 @@
 //  * Softmax runs in base 2 (scores pre-multiplied by scale*log2(e)); the
 //    running-max rescale of the accumulator is skipped when no lane's max
 //    moved.
-//  * The split merge is fused: each workgroup writes its (m, l, O) partial,
-//    and the last workgroup of a kv head to arrive (device-scope counter)
-//    merges all splits and writes the output, then re-arms the counter.
+//  * Each workgroup writes its split's (m, l, O) partial; a second small
+//    kernel merges the splits of every q head with one round of loads (each
+//    thread folds a strided subset of splits, then the subsets merge in LDS).
+//    The scratch layout is the reference's ([Hq,S] m, [Hq,S] l,
+//    [Hq,S,D] acc); it needs no initialization.
 //  * Workgroups of one split for all kv heads land on one XCD, so the
 //    interleaved [token, kv_head] scale lines are fetched into one L2.
 //
 // The key range of split si is [si*per, min(si*per+per, n_keys)) with
-// per = 32 * ceil(ceil(n_keys / S) / 32); splits past the last key exit
-// before touching the counter. n_keys = *cache_len + 1 is read on device, so
+// per = 32 * ceil(ceil(n_keys / S) / 32); splits past the last key exit at
+// once and the merge skips them. n_keys = *cache_len + 1 is read on device, so
 // one launch configuration serves every decode step (graph capturable).
 #include "device_common.hpp"
 #include "launch.hpp"
@@ -38,6 +40,7 @@ constexpr int kDecWaves   = 8;
 constexpr int kDecThreads = kDecWaves * kWave;
 constexpr int kTileKeys   = 32;     // keys per wave iteration (two 16-key MFMAs)
 constexpr int kMaxGroupD  = 2048;   // G * head_dim bound of the LDS wave merge
+constexpr int kCombineThreads = 256;
 
 template <int D>
 struct DecTraits {
@@ -47,6 +50,7 @@ struct DecTraits {
     static constexpr int kVBytes  = D / 16;   // V bytes per lane per key
     static constexpr int kVWords  = kVBytes / 4;
     static constexpr int kOMfma   = D / 16;   // PV MFMAs, one per d offset c
+    static constexpr int kRing    = 2;  // register tiles in flight (deeper measured slower)
 };
 
 // One tile's raw global data held by a lane.
@@ -54,7 +58,7 @@ template <int D>
 struct TileRaw {
     u32x4    kraw[2][DecTraits<D>::kKChunks];
     uint32_t vraw[8][DecTraits<D>::kVWords];
-    float    sc;
+    float    sc;       // lane l < 32: k_scale of key l, else v_scale of key l - 32
 };
 
 __device__ __forceinline__ int key_of(int g, int j) {  // P^T k-index -> key in tile
@@ -98,30 +102,28 @@ __device__ __forceinline__ void load_tile(TileRaw<D>& t, const uint8_t* __restri
         }
     }
     {
-        const int key = min(kb + (lane & 31), k1 - 1);
+        const int     key = min(kb + (lane & 31), k1 - 1);
         const int64_t row = static_cast<int64_t>(key) * hkv + kvh;
-        t.sc = (lane < 32) ? ks[row] : vs[row];
+        t.sc              = (lane < 32) ? ks[row] : vs[row];
     }
 }
 
 template <int D>
 __global__ __launch_bounds__(kDecThreads) void flash_decode_kernel(
-    uint16_t* __restrict__ out, const uint16_t* __restrict__ q,
-    const uint8_t* __restrict__ k, const uint8_t* __restrict__ v,
-    const float* __restrict__ ks, const float* __restrict__ vs,
-    float* __restrict__ partial, int num_splits, const int* __restrict__ cache_len,
-    int hq, int hkv, float scale_log2) {
+    const uint16_t* __restrict__ q, const uint8_t* __restrict__ k,
+    const uint8_t* __restrict__ v, const float* __restrict__ ks,
+    const float* __restrict__ vs, float* __restrict__ partial, int num_splits,
+    const int* __restrict__ cache_len, int hq, int hkv, float scale_log2) {
     using T = DecTraits<D>;
 
-    __shared__ float sm_sc[kDecWaves][64];
+    __shared__ __attribute__((aligned(16))) float sm_sc[kDecWaves][64];
     __shared__ float sm_m[kDecWaves][16];
     __shared__ float sm_l[kDecWaves][16];
-    __shared__ float sm_o[kDecWaves * kMaxGroupD];
-    __shared__ int   sm_last;
+    __shared__ __attribute__((aligned(16))) float sm_o[kDecWaves * kMaxGroupD];
 
     const int G    = hq / hkv;
     const int tid  = static_cast<int>(threadIdx.x);
-    const int wave = tid / kWave;
+    const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
     const int lane = tid & (kWave - 1);
     const int n    = lane & 15;
     const int g    = lane >> 4;
@@ -175,21 +177,15 @@ __global__ __launch_bounds__(kDecThreads) void flash_decode_kernel(
     float m_run = -INFINITY;
     float l_run = 0.0f;
 
-    TileRaw<D> cur, nxt;
-    int        t = wave;
-    if (t < n_tiles) {
-        load_tile<D>(cur, k, v, ks, vs, k0 + t * kTileKeys, k1, kvh, hkv, lane);
-    }
-    for (; t < n_tiles; t += kDecWaves) {
-        const int kb = k0 + t * kTileKeys;
-        if (t + kDecWaves < n_tiles) {
-            load_tile<D>(nxt, k, v, ks, vs, kb + kDecWaves * kTileKeys, k1, kvh, hkv, lane);
-        }
-
-        // Per-key factors: [0,32) = k_scale * scale * log2(e), [32,64) = v_scale.
-        sm_sc[wave][lane] = (lane < 32) ? cur.sc * scale_log2 : cur.sc;
+    // Softmax state: m_ref is this lane's head reference maximum (shared by the
+    // four lanes of a head); scores are exponentiated against it. It is raised
+    // only when some score exceeds it by more than 2^kLazy, so the usual tile
+    // needs no cross-lane step and no accumulator rescale. Exact: every p and
+    // l use the same reference, and p <= 2^kLazy keeps them in range.
+    constexpr float kLazy = 8.0f;
+    auto process = [&](const TileRaw<D>& cur, const int kb) {
+        sm_sc[wave][lane] = cur.sc;
         __builtin_amdgcn_wave_barrier();
-
         // S^T = K Q^T, two 16-key halves.
         f32x4 s[2];
 #pragma unroll
@@ -204,16 +200,17 @@ __global__ __launch_bounds__(kDecThreads) void flash_decode_kernel(
             }
         }
 
+        // Register j of this lane is key key_of(g, j) of the tile; its scales
+        // come from the lanes that loaded them, through this wave's LDS row.
         const f32x4 kf0 = *reinterpret_cast<const f32x4*>(&sm_sc[wave][4 * g]);
         const f32x4 kf1 = *reinterpret_cast<const f32x4*>(&sm_sc[wave][16 + 4 * g]);
         const f32x4 vf0 = *reinterpret_cast<const f32x4*>(&sm_sc[wave][32 + 4 * g]);
         const f32x4 vf1 = *reinterpret_cast<const f32x4*>(&sm_sc[wave][48 + 4 * g]);
-
         float x[8];
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-            x[r]     = s[0][r] * kf0[r];
-            x[4 + r] = s[1][r] * kf1[r];
+            x[r]     = s[0][r] * (kf0[r] * scale_log2);
+            x[4 + r] = s[1][r] * (kf1[r] * scale_log2);
         }
         if (kb + kTileKeys > k1) {  // ragged last tile of the split
 #pragma unroll
@@ -223,31 +220,26 @@ __global__ __launch_bounds__(kDecThreads) void flash_decode_kernel(
                 }
             }
         }
-        float tmax = x[0];
-#pragma unroll
-        for (int j = 1; j < 8; ++j) {
-            tmax = fmaxf(tmax, x[j]);
-        }
-        tmax = wave_xor_max(tmax, 16);
-        tmax = wave_xor_max(tmax, 32);
-
-        const float m_new = fmaxf(m_run, tmax);
-        const float alpha = exp2f(m_run - m_new);
-        float       p[8];
-        float       psum = 0.0f;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            p[j] = exp2f(x[j] - m_new);
-            psum += p[j];
-        }
-        l_run = l_run * alpha + psum;
-        m_run = m_new;
-        if (__any(alpha != 1.0f)) {
+        float lmax = fmaxf(fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3])),
+                           fmaxf(fmaxf(x[4], x[5]), fmaxf(x[6], x[7])));
+        if (!__all(lmax <= m_run + kLazy)) {
+            lmax              = wave_xor_max(lmax, 16);
+            lmax              = wave_xor_max(lmax, 32);
+            const float m_new = fmaxf(m_run, lmax);
+            const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+            l_run *= alpha;
 #pragma unroll
             for (int c = 0; c < T::kOMfma; ++c) {
                 oacc[c] *= alpha;
             }
+            m_run = m_new;
         }
+        float p[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            p[j] = __builtin_amdgcn_exp2f(x[j] - m_run);
+        }
+        l_run += ((p[0] + p[1]) + (p[2] + p[3])) + ((p[4] + p[5]) + (p[6] + p[7]));
 
         u32x4 pw;
         pw.x = pack_bf16x2(p[0] * vf0[0], p[1] * vf0[1]);
@@ -280,7 +272,40 @@ __global__ __launch_bounds__(kDecThreads) void flash_decode_kernel(
                 __builtin_bit_cast(bf16x8, aw), pop, oacc[c], 0, 0, 0);
         }
         __builtin_amdgcn_wave_barrier();
-        cur = nxt;
+    };
+
+    // Ring of kRing register tiles: the load of tile i + kRing - 1 is issued
+    // before tile i is consumed, with compile-time buffer indices and no
+    // branch in between, so kRing - 1 tiles stay in flight per wave while it
+    // computes (the memory latency under full load is several microseconds).
+    // Tile indices past the split's last tile are clamped to it; those
+    // reloads hit in L2 and are never consumed.
+    constexpr int kRing     = DecTraits<D>::kRing;
+    const int     last_tile = n_tiles - 1;
+    if (wave <= last_tile) {
+        TileRaw<D> ring[kRing];
+#pragma unroll
+        for (int r = 0; r + 1 < kRing; ++r) {
+            load_tile<D>(ring[r], k, v, ks, vs, k0 + min(wave + r * kDecWaves, last_tile) * kTileKeys,
+                         k1, kvh, hkv, lane);
+        }
+        for (int t = wave;; t += kRing * kDecWaves) {
+            bool done = false;
+#pragma unroll
+            for (int r = 0; r < kRing; ++r) {
+                if (!done) {
+                    const int tr = t + r * kDecWaves;
+                    load_tile<D>(ring[(r + kRing - 1) % kRing], k, v, ks, vs,
+                                 k0 + min(tr + (kRing - 1) * kDecWaves, last_tile) * kTileKeys,
+                                 k1, kvh, hkv, lane);
+                    process(ring[r], k0 + tr * kTileKeys);
+                    done = tr + kDecWaves > last_tile;
+                }
+            }
+            if (done) {
+                break;
+            }
+        }
     }
 
     // ---- merge the waves of this workgroup --------------------------------
@@ -310,20 +335,22 @@ __global__ __launch_bounds__(kDecThreads) void flash_decode_kernel(
     }
     __syncthreads();
 
+    // Partial of this split, reference layout: m at [h*S + si] (log2 units),
+    // l at [Hq*S + h*S + si], acc at [2*Hq*S + (h*S + si)*D + d].
     const int64_t hs     = static_cast<int64_t>(hq) * num_splits;
-    const int64_t slot0  = (static_cast<int64_t>(kvh) * num_splits + si) * G;
     float*        part_m = partial;
     float*        part_l = partial + hs;
     float*        part_o = partial + 2 * hs;
-    for (int e = tid; e < G * D; e += kDecThreads) {
-        const int h = e / D;
-        const int d = e - h * D;
-        float     a = 0.0f;
+    for (int e = tid; e < G * (D / 4); e += kDecThreads) {
+        const int h  = e / (D / 4);
+        const int d0 = 4 * (e - h * (D / 4));
+        f32x4     a  = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int w = 0; w < kDecWaves; ++w) {
-            a += sm_o[(w * G + h) * D + d];
+            a += *reinterpret_cast<const f32x4*>(&sm_o[(w * G + h) * D + d0]);
         }
-        part_o[(slot0 + h) * D + d] = a;
+        const int64_t slot = static_cast<int64_t>(kvh * G + h) * num_splits + si;
+        *reinterpret_cast<f32x4*>(&part_o[slot * D + d0]) = a;
     }
     if (tid < G) {
         float M = -INFINITY;
@@ -335,49 +362,99 @@ __global__ __launch_bounds__(kDecThreads) void flash_decode_kernel(
             const float mw = sm_m[w][tid];
             L += (mw == -INFINITY) ? 0.0f : sm_l[w][tid] * exp2f(mw - M);
         }
-        part_m[slot0 + tid] = M;
-        part_l[slot0 + tid] = L;
-    }
-
-    // ---- last arrival merges the splits of this kv head -------------------
-    int* counters = reinterpret_cast<int*>(partial + hs * (D + 2));
-    __threadfence();
-    __syncthreads();
-    if (tid == 0) {
-        const int prev = atomicAdd(&counters[kvh], 1);
-        sm_last        = (prev == n_eff - 1) ? 1 : 0;
-    }
-    __syncthreads();
-    if (!sm_last) {
-        return;
-    }
-    __threadfence();
-
-    const int64_t base = static_cast<int64_t>(kvh) * num_splits * G;
-    for (int e = tid; e < G * D; e += kDecThreads) {
-        const int h = e / D;
-        const int d = e - h * D;
-        float     M = -INFINITY;
-        for (int s = 0; s < n_eff; ++s) {
-            M = fmaxf(M, part_m[base + s * G + h]);
-        }
-        float acc = 0.0f, L = 0.0f;
-        for (int s = 0; s < n_eff; ++s) {
-            const float f = exp2f(part_m[base + s * G + h] - M);
-            L += f * part_l[base + s * G + h];
-            acc += f * part_o[(base + s * G + h) * D + d];
-        }
-        out[static_cast<int64_t>(kvh * G + h) * D + d] = f32_to_bf16_bits(acc / L);
-    }
-    if (tid == 0) {
-        counters[kvh] = 0;
+        const int64_t slot = static_cast<int64_t>(kvh * G + tid) * num_splits + si;
+        part_m[slot]       = M;
+        part_l[slot]       = L;
     }
 }
 
-__global__ void zero_ints_kernel(int* p, int n) {
-    const int i = static_cast<int>(blockIdx.x * blockDim.x + threadIdx.x);
-    if (i < n) {
-        p[i] = 0;
+// One workgroup per q head: merges the n_eff split partials,
+// out = sum_s 2^(m_s - M) acc_s / sum_s 2^(m_s - M) l_s (reference
+// src/kernels/flash_decode.cu:222-247). Thread (group g, quad q) folds
+// splits g, g + kGroups, ... for d = 4q .. 4q+3 with an online max, so every
+// load is issued up front; the kGroups states merge through LDS.
+template <int D>
+__global__ __launch_bounds__(kCombineThreads) void flash_decode_combine_kernel(
+    uint16_t* __restrict__ out, const float* __restrict__ partial, int num_splits,
+    const int* __restrict__ cache_len, int hq) {
+    constexpr int kQuads  = D / 4;
+    constexpr int kGroups = kCombineThreads / kQuads;
+    __shared__ __attribute__((aligned(16))) f32x4 sm_acc[kGroups][kQuads];
+    __shared__ float sm_mm[kGroups], sm_ll[kGroups];
+
+    const int qh  = static_cast<int>(blockIdx.x);
+    const int tid = static_cast<int>(threadIdx.x);
+    const int grp = tid / kQuads;
+    const int qd  = tid - grp * kQuads;
+
+    const int n_keys = *cache_len + 1;
+    int       per    = (n_keys + num_splits - 1) / num_splits;
+    per              = (per + kTileKeys - 1) & ~(kTileKeys - 1);
+    const int n_eff  = (n_keys + per - 1) / per;
+
+    const int64_t hs     = static_cast<int64_t>(hq) * num_splits;
+    const float*  part_m = partial + static_cast<int64_t>(qh) * num_splits;
+    const float*  part_l = partial + hs + static_cast<int64_t>(qh) * num_splits;
+    const float*  part_o = partial + 2 * hs + static_cast<int64_t>(qh) * num_splits * D;
+
+    float m = -INFINITY, l = 0.0f;
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    for (int s0 = grp; s0 < n_eff; s0 += 8 * kGroups) {
+        float ms[8], ls[8];
+        f32x4 os[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const int s = s0 + u * kGroups;
+            ms[u]       = -INFINITY;
+            ls[u]       = 0.0f;
+            os[u]       = f32x4{0.f, 0.f, 0.f, 0.f};
+            if (s < n_eff) {
+                ms[u] = part_m[s];
+                ls[u] = part_l[s];
+                os[u] = *reinterpret_cast<const f32x4*>(&part_o[static_cast<int64_t>(s) * D + 4 * qd]);
+            }
+        }
+        float mx = m;
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            mx = fmaxf(mx, ms[u]);
+        }
+        const float c = (m == -INFINITY) ? 0.0f : exp2f(m - mx);
+        acc *= c;
+        l *= c;
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const float f = (ms[u] == -INFINITY) ? 0.0f : exp2f(ms[u] - mx);
+            acc += os[u] * f;
+            l += ls[u] * f;
+        }
+        m = mx;
+    }
+    if (qd == 0) {
+        sm_mm[grp] = m;
+        sm_ll[grp] = l;
+    }
+    sm_acc[grp][qd] = acc;
+    __syncthreads();
+    if (grp == 0) {
+        float M = -INFINITY;
+#pragma unroll
+        for (int g2 = 0; g2 < kGroups; ++g2) {
+            M = fmaxf(M, sm_mm[g2]);
+        }
+        f32x4 t = {0.f, 0.f, 0.f, 0.f};
+        float L = 0.0f;
+#pragma unroll
+        for (int g2 = 0; g2 < kGroups; ++g2) {
+            const float f = (sm_mm[g2] == -INFINITY) ? 0.0f : exp2f(sm_mm[g2] - M);
+            t += sm_acc[g2][qd] * f;
+            L += sm_ll[g2] * f;
+        }
+        const float inv = 1.0f / L;
+        u32x2       w2;
+        w2.x = pack_bf16x2(t[0] * inv, t[1] * inv);
+        w2.y = pack_bf16x2(t[2] * inv, t[3] * inv);
+        *reinterpret_cast<u32x2*>(out + static_cast<int64_t>(qh) * D + 4 * qd) = w2;
     }
 }
 
@@ -394,8 +471,15 @@ hipError_t launch_decode(uint16_t* out, const uint16_t* q, const uint8_t* k,
                          int hq, int hkv, float scale, hipStream_t stream) {
     const dim3 grid(static_cast<unsigned>(num_splits * hkv));
     hipLaunchKernelGGL(flash_decode_kernel<D>, grid, dim3(kDecThreads), 0, stream,
-                       out, q, k, v, ks, vs, partial, num_splits, cache_len, hq,
-                       hkv, scale * kLog2e);
+                       q, k, v, ks, vs, partial, num_splits, cache_len, hq, hkv,
+                       scale * kLog2e);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) {
+        return e;
+    }
+    hipLaunchKernelGGL(flash_decode_combine_kernel<D>, dim3(static_cast<unsigned>(hq)),
+                       dim3(kCombineThreads), 0, stream, out, partial, num_splits,
+                       cache_len, hq);
     return hipGetLastError();
 }
 
@@ -404,19 +488,7 @@ hipError_t launch_decode(uint16_t* out, const uint16_t* q, const uint8_t* k,
 std::size_t decode_scratch_floats(int num_q_heads, int head_dim, int max_splits) {
     const std::size_t hs = static_cast<std::size_t>(num_q_heads) *
                            static_cast<std::size_t>(max_splits);
-    const std::size_t counters = (static_cast<std::size_t>(num_q_heads) + 63) / 64 * 64;
-    return hs * (static_cast<std::size_t>(head_dim) + 2) + counters;
-}
-
-hipError_t decode_scratch_reset_launch(float* partial, int num_q_heads,
-                                       int head_dim, int max_splits,
-                                       hipStream_t stream) {
-    const std::size_t hs = static_cast<std::size_t>(num_q_heads) *
-                           static_cast<std::size_t>(max_splits);
-    int* counters = reinterpret_cast<int*>(partial + hs * (head_dim + 2));
-    hipLaunchKernelGGL(zero_ints_kernel, dim3((num_q_heads + 255) / 256), dim3(256), 0,
-                       stream, counters, num_q_heads);
-    return hipGetLastError();
+    return hs * 2 + hs * static_cast<std::size_t>(head_dim);
 }
 
 bool decode_mfma_supported(int num_q_heads, int num_kv_heads, int head_dim) {

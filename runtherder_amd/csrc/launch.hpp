@@ -25,13 +25,8 @@ hipError_t kv_append_fp8_launch(uint8_t* k_q, uint8_t* v_q, float* k_scale,
                                 int rows_per_pos, int num_rows, int head_dim,
                                 hipStream_t stream);
 
-// Split-K decode scratch: per (kv head, split) partial softmax state followed
-// by one arrival counter per kv head. Sized in floats.
+// Split-K decode scratch in floats: [Hq, S] m, [Hq, S] l, [Hq, S, D] acc.
 std::size_t decode_scratch_floats(int num_q_heads, int head_dim, int max_splits);
-
-hipError_t decode_scratch_reset_launch(float* partial, int num_q_heads,
-                                       int head_dim, int max_splits,
-                                       hipStream_t stream);
 
 hipError_t flash_decode_launch(uint16_t* out, const uint16_t* q,
                                const uint8_t* k, const uint8_t* v,

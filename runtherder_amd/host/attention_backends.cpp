@@ -32,10 +32,6 @@ AdaptiveAttention::AdaptiveAttention(const AttnConfig& config, int num_splits)
     RUNTHERDER_CHECK(num_splits >= 1, "AdaptiveAttention num_splits must be >= 1");
     partial_ = device::make_device_unique<float>(
         rth_split_scratch_floats(config.num_q_heads, config.head_dim, num_splits));
-    // The decode kernel's arrival counters start at zero and are left at zero.
-    RUNTHERDER_RTH_CHECK(rth_split_scratch_init(partial_.get(), config.num_q_heads,
-                                                config.head_dim, num_splits, nullptr));
-    RUNTHERDER_HIP_CHECK(hipDeviceSynchronize());
 }
 
 void AdaptiveAttention::run(__hip_bfloat16* out, const __hip_bfloat16* q, const KVView& kv,

@@ -61,17 +61,14 @@ def quantize_kv_fp8_scaled(q, scale, x, at_pos, rows_per_pos, num_rows, head_dim
 
 
 def flash_split_scratch_floats(num_q_heads: int, head_dim: int, max_splits: int) -> int:
-    """reference include/runtherder/kernels/flash_decode.cuh:16-24 (+ counters)"""
+    """reference include/runtherder/kernels/flash_decode.cuh:16-24"""
     return int(_ffi.load().rth_split_scratch_floats(num_q_heads, head_dim, max_splits))
 
 
-def new_flash_split_scratch(num_q_heads, head_dim, max_splits, device="cuda", stream=None):
-    """Allocates decode scratch and zeroes its arrival counters."""
+def new_flash_split_scratch(num_q_heads, head_dim, max_splits, device="cuda"):
+    """Allocates decode scratch (no initialization needed)."""
     n = flash_split_scratch_floats(num_q_heads, head_dim, max_splits)
-    t = torch.empty(n, dtype=torch.float32, device=device)
-    _ffi.call("rth_split_scratch_init", _p(t), num_q_heads, head_dim, max_splits,
-              _stream(stream))
-    return t
+    return torch.empty(n, dtype=torch.float32, device=device)
 
 
 def default_num_splits(num_kv_heads: int, device: int = 0) -> int:

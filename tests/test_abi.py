@@ -69,9 +69,9 @@ def test_naive_rejects_large_head_dim():
 
 
 def test_scratch_size_formula():
-    # reference formula Hq*S*2 + Hq*S*D, plus counters rounded up to 64
-    assert R.flash_split_scratch_floats(32, 128, 64) == 32 * 64 * 2 + 32 * 64 * 128 + 64
-    assert R.flash_split_scratch_floats(24, 128, 32) == 24 * 32 * 130 + 64
+    # reference formula Hq*S*2 + Hq*S*D (flash_decode.cuh:16-24)
+    assert R.flash_split_scratch_floats(32, 128, 64) == 32 * 64 * 2 + 32 * 64 * 128
+    assert R.flash_split_scratch_floats(24, 128, 32) == 24 * 32 * 130
     assert _ffi.load().rth_split_scratch_floats(0, 128, 4) == 0
 
 

@@ -122,9 +122,9 @@ def test_config5_long_context_per_head_scales():
     check(got, q, k8, v8, ks, vs, ctx - 1, hq, hkv, d, scale)
 
 
-def test_repeated_calls_rearm_counters():
-    """The fused merge re-arms its counters: back-to-back calls with
-    different depths on one scratch stay correct."""
+def test_repeated_calls_share_scratch():
+    """Back-to-back calls with different depths on one scratch stay correct
+    (the scratch carries no state between calls)."""
     hq, hkv, d = 32, 8, 128
     scale = np.float32(1.0 / np.sqrt(d))
     total = 3000
