@@ -67,8 +67,8 @@ __device__ __forceinline__ void pf_load(PfRaw& r, const uint8_t* __restrict__ k,
         r.k[1] = *reinterpret_cast<const u32x4*>(kr + 16);
     }
     {
-        const int kq = tid >> 4;           // key quad 0..15
-        const int d0 = 8 * (tid & 15);
+        const int kq = tid & 15;           // key quad 0..15
+        const int d0 = 8 * (tid >> 4);     // 8 d of those 4 keys
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             const int key = min(key0 + 4 * kq + j, total - 1);
@@ -99,8 +99,11 @@ __device__ __forceinline__ void pf_stage(const PfRaw& r, uint16_t* sK, uint16_t*
         *reinterpret_cast<bf16x8*>(dst + 24) = d;
     }
     {
-        const int kq = tid >> 4;
-        const int d0 = 8 * (tid & 15);
+        // Lanes 16i..16i+15 share d0 and cover the 16 key quads, so each
+        // 16-lane pass of the 8-byte LDS writes fills one whole V^T row
+        // (bank-conflict free).
+        const int kq = tid & 15;
+        const int d0 = 8 * (tid >> 4);
         // 4 keys x 8 bytes -> 8 dwords, each holding one d for the 4 keys.
         uint32_t x[8];
 #pragma unroll
@@ -142,7 +145,7 @@ __global__ __launch_bounds__(kPfThreads, 2) void flash_prefill_kernel(
     __shared__ __attribute__((aligned(16))) float    sVf[kBN];
 
     const int tid  = static_cast<int>(threadIdx.x);
-    const int wave = tid / kWave;
+    const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
     const int lane = tid & (kWave - 1);
     const int qn   = lane & 31;   // query row of this lane within the wave
     const int h    = lane >> 5;   // k-group
@@ -219,34 +222,61 @@ __global__ __launch_bounds__(kPfThreads, 2) void flash_prefill_kernel(
             }
         }
 
-        // Column factors and masking. Register r of block kb is key
-        // 32kb + 8(r/4) + 4h + r%4 of the tile.
-        const bool need_mask = (key0 + kBN - 1 > clen + wq0) || (key0 + kBN > total);
-        float      tmax      = -INFINITY;
+        // t = s * (k_scale * scale * log2 e) - m_ref, one fma per score.
+        // Register r of block kb is key 32kb + 8(r/4) + 4h + r%4 of the tile.
+        const float base = (m_run == -INFINITY) ? 0.0f : m_run;
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb) {
 #pragma unroll
             for (int rg = 0; rg < 4; ++rg) {
-                const int   kofs = 32 * kb + 8 * rg + 4 * h;
-                const f32x4 kf   = *reinterpret_cast<const f32x4*>(sKf + kofs);
+                const f32x4 kf = *reinterpret_cast<const f32x4*>(sKf + 32 * kb + 8 * rg + 4 * h);
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
-                    float x = s[kb][4 * rg + e] * kf[e];
-                    if (need_mask) {
-                        const int kp = key0 + kofs + e;
-                        if (kp > my_pos || kp >= total) {
-                            x = -INFINITY;
-                        }
-                    }
-                    s[kb][4 * rg + e] = x;
-                    tmax              = fmaxf(tmax, x);
+                    s[kb][4 * rg + e] = fmaf(s[kb][4 * rg + e], kf[e], -base);
                 }
             }
         }
-        tmax = wave_xor_max(tmax, 32);
-        const float m_new = fmaxf(m_run, tmax);
-        const float alpha = exp2f(m_run - m_new);
-        m_run             = m_new;
+        // Causal / key-end mask, only on tiles that cross the diagonal or the
+        // end of the keys (a wave-uniform branch).
+        if ((key0 + kBN - 1 > clen + wq0) || (key0 + kBN > total)) {
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb) {
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int kp = key0 + 32 * kb + 8 * (r >> 2) + 4 * h + (r & 3);
+                    if (kp > my_pos || kp >= total) {
+                        s[kb][r] = -INFINITY;
+                    }
+                }
+            }
+        }
+        float tmax = -INFINITY;
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                tmax = fmaxf(tmax, s[kb][r]);
+            }
+        }
+        // Lazy reference max (exact): scores are exponentiated against m_run,
+        // raised only when one exceeds it by more than 2^8, so most tiles need
+        // no cross-lane step and no O rescale.
+        if (!__all((tmax <= 8.0f) && (m_run != -INFINITY))) {
+            tmax              = wave_xor_max(tmax, 32);
+            const float m_new = fmaxf(m_run, base + tmax);
+            const float delta = m_new - base;
+            const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb) {
+                s[kb] -= delta;
+            }
+            l_run *= alpha;
+#pragma unroll
+            for (int db = 0; db < 4; ++db) {
+                o[db] *= alpha;
+            }
+            m_run = m_new;
+        }
 
         bf16x8 pop[4];
         float  psum = 0.0f;
@@ -259,10 +289,10 @@ __global__ __launch_bounds__(kPfThreads, 2) void flash_prefill_kernel(
                 for (int rr = 0; rr < 2; ++rr) {
                     const int   rg   = 2 * half + rr;
                     const f32x4 vf   = *reinterpret_cast<const f32x4*>(sVf + 32 * kb + 8 * rg + 4 * h);
-                    const float p0   = exp2f(s[kb][4 * rg + 0] - m_new);
-                    const float p1   = exp2f(s[kb][4 * rg + 1] - m_new);
-                    const float p2   = exp2f(s[kb][4 * rg + 2] - m_new);
-                    const float p3   = exp2f(s[kb][4 * rg + 3] - m_new);
+                    const float p0   = __builtin_amdgcn_exp2f(s[kb][4 * rg + 0]);
+                    const float p1   = __builtin_amdgcn_exp2f(s[kb][4 * rg + 1]);
+                    const float p2   = __builtin_amdgcn_exp2f(s[kb][4 * rg + 2]);
+                    const float p3   = __builtin_amdgcn_exp2f(s[kb][4 * rg + 3]);
                     psum += (p0 + p1) + (p2 + p3);
                     pw[2 * rr]     = pack_bf16x2(p0 * vf[0], p1 * vf[1]);
                     pw[2 * rr + 1] = pack_bf16x2(p2 * vf[2], p3 * vf[3]);
@@ -270,13 +300,7 @@ __global__ __launch_bounds__(kPfThreads, 2) void flash_prefill_kernel(
                 pop[2 * kb + half] = __builtin_bit_cast(bf16x8, pw);
             }
         }
-        l_run = l_run * alpha + psum;
-        if (__any(alpha != 1.0f)) {
-#pragma unroll
-            for (int db = 0; db < 4; ++db) {
-                o[db] *= alpha;
-            }
-        }
+        l_run += psum;
 
         // O^T += V^T P^T.
 #pragma unroll
