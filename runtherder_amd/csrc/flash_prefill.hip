@@ -209,17 +209,34 @@ __global__ __launch_bounds__(kPfThreads, 2) void flash_prefill_kernel(
         }
         const int key0 = kt * kBN;
 
-        // S^T = K Q^T for two 32-key blocks.
+        // S^T = K Q^T for two 32-key blocks. The LDS operand reads run four
+        // MFMAs ahead (scheduling groups), so their latency is hidden.
         f32x16 s[2];
+        {
+            bf16x8 ka[2][8];
 #pragma unroll
-        for (int kb = 0; kb < 2; ++kb) {
-            s[kb] = f32x16{};
-            const uint16_t* arow = sK + (32 * kb + qn) * kKPitch + 8 * h;
+            for (int kb = 0; kb < 2; ++kb) {
+                const uint16_t* arow = sK + (32 * kb + qn) * kKPitch + 8 * h;
 #pragma unroll
-            for (int st = 0; st < 8; ++st) {
-                const bf16x8 a = *reinterpret_cast<const bf16x8*>(arow + 16 * st);
-                s[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qop[st], s[kb], 0, 0, 0);
+                for (int st = 0; st < 8; ++st) {
+                    ka[kb][st] = *reinterpret_cast<const bf16x8*>(arow + 16 * st);
+                }
             }
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb) {
+                s[kb] = f32x16{};
+#pragma unroll
+                for (int st = 0; st < 8; ++st) {
+                    s[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ka[kb][st], qop[st], s[kb], 0, 0, 0);
+                }
+            }
+            __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+#pragma unroll
+            for (int i = 0; i < 12; ++i) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+            }
+            __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
         }
 
         // t = s * (k_scale * scale * log2 e) - m_ref, one fma per score.
@@ -302,15 +319,31 @@ __global__ __launch_bounds__(kPfThreads, 2) void flash_prefill_kernel(
         }
         l_run += psum;
 
-        // O^T += V^T P^T.
+        // O^T += V^T P^T, operand reads four MFMAs ahead as above.
+        {
+            bf16x8 va[4][4];
 #pragma unroll
-        for (int db = 0; db < 4; ++db) {
-            const uint16_t* arow = sVt + (32 * db + qn) * kVPitch + 8 * h;
+            for (int db = 0; db < 4; ++db) {
+                const uint16_t* arow = sVt + (32 * db + qn) * kVPitch + 8 * h;
 #pragma unroll
-            for (int t = 0; t < 4; ++t) {
-                const bf16x8 a = *reinterpret_cast<const bf16x8*>(arow + 16 * t);
-                o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, pop[t], o[db], 0, 0, 0);
+                for (int t = 0; t < 4; ++t) {
+                    va[db][t] = *reinterpret_cast<const bf16x8*>(arow + 16 * t);
+                }
             }
+#pragma unroll
+            for (int db = 0; db < 4; ++db) {
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+                    o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va[db][t], pop[t], o[db], 0, 0, 0);
+                }
+            }
+            __builtin_amdgcn_sched_group_barrier(0x100, 4, 1);
+#pragma unroll
+            for (int i = 0; i < 12; ++i) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);
+                __builtin_amdgcn_sched_group_barrier(0x100, 1, 1);
+            }
+            __builtin_amdgcn_sched_group_barrier(0x008, 4, 1);
         }
     }
 

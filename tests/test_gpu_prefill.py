@@ -147,7 +147,9 @@ def test_chunked_prefill_equals_full_tail():
                          view.v_scale, total - clen, int_dev(clen), hq, hkv, d, scale)
     sync()
     mx, mean = O.bf16_err(bf16_host(full)[clen:], bf16_host(tail))
-    assert mx <= 1e-2 and mean <= 1e-3, (mx, mean)
+    # The two launches sum in different orders (different tile boundaries), so
+    # they may differ by a bf16 ulp; the bar is the attention tolerance.
+    assert mx <= MAX_ABS and mean <= 1e-4, (mx, mean)
 
 
 def test_config5_chunked_prefill_into_128k_cache():
