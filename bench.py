@@ -340,8 +340,8 @@ def main() -> int:
     ap.add_argument("--ctx", type=int, default=8196)
     ap.add_argument("--prefill-n", type=int, default=4096)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--sweep", action="store_true",
-                    help="per-call decode and prefill sweeps over the BASELINE depths")
+    ap.add_argument("--sweep", nargs="?", const="all", choices=("all", "decode", "prefill"),
+                    help="per-call decode and/or prefill sweeps over the BASELINE depths")
     ap.add_argument("--mode", choices=("full", "kernels", "copy"), default="full",
                     help="kernels: eager launches of the bench kernels only (for "
                          "rocprofv3 --pmc); copy: a 256 MiB device copy (PMC "
@@ -363,10 +363,12 @@ def main() -> int:
     if args.mode == "kernels":
         return eager_kernels(torch, R, stream, args)
     if args.sweep:
-        decode_kernel_sweep(torch, R, stream, [(24, 8, 35, None), (24, 8, 2041, None),
-                                               (24, 8, 8196, None), (24, 8, 32768, None),
-                                               (32, 8, 131072, 64)])
-        prefill_sweep(torch, R, stream, [1021, 2048, 4096, 8192, 16384])
+        if args.sweep != "prefill":
+            decode_kernel_sweep(torch, R, stream, [(24, 8, 35, None), (24, 8, 2041, None),
+                                                   (24, 8, 8196, None), (24, 8, 32768, None),
+                                                   (32, 8, 131072, 64)])
+        if args.sweep != "decode":
+            prefill_sweep(torch, R, stream, [1021, 2048, 4096, 8192, 16384])
         return 0
     dec = bench_decode(torch, R, args, stream)
     pf = bench_prefill(torch, R, stream, n=args.prefill_n)

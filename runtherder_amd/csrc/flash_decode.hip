@@ -140,18 +140,8 @@ __global__ __launch_bounds__(kDecThreads) void flash_decode_kernel(
         kvh = bid % hkv;
     }
 
-    const int n_keys = *cache_len + 1;
-    int       per    = (n_keys + num_splits - 1) / num_splits;
-    per              = (per + kTileKeys - 1) & ~(kTileKeys - 1);
-    const int n_eff  = (n_keys + per - 1) / per;
-    if (si >= n_eff) {
-        return;
-    }
-    const int k0      = si * per;
-    const int k1      = min(k0 + per, n_keys);
-    const int n_tiles = (k1 - k0 + kTileKeys - 1) / kTileKeys;
-
     // Q^T as the B operand: column n = q head of the group (zero past G).
+    // Loaded before cache_len is known, so both loads are in flight together.
     bf16x8 qop[T::kKSteps];
     {
         const bool      has = n < G;
@@ -168,6 +158,17 @@ __global__ __launch_bounds__(kDecThreads) void flash_decode_kernel(
             }
         }
     }
+
+    const int n_keys = *cache_len + 1;
+    int       per    = (n_keys + num_splits - 1) / num_splits;
+    per              = (per + kTileKeys - 1) & ~(kTileKeys - 1);
+    const int n_eff  = (n_keys + per - 1) / per;
+    if (si >= n_eff) {
+        return;
+    }
+    const int k0      = si * per;
+    const int k1      = min(k0 + per, n_keys);
+    const int n_tiles = (k1 - k0 + kTileKeys - 1) / kTileKeys;
 
     f32x4 oacc[T::kOMfma];
 #pragma unroll
@@ -399,7 +400,10 @@ __global__ __launch_bounds__(kCombineThreads) void flash_decode_combine_kernel(
 
     float m = -INFINITY, l = 0.0f;
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-    for (int s0 = grp; s0 < n_eff; s0 += 8 * kGroups) {
+    // Slots are loaded up to num_splits, in flight with the cache_len load;
+    // slots at or past n_eff hold stale data and are replaced by selects (not
+    // multiplied by zero, which would keep a stale NaN).
+    for (int s0 = grp; s0 < num_splits; s0 += 8 * kGroups) {
         float ms[8], ls[8];
         f32x4 os[8];
 #pragma unroll
@@ -408,11 +412,18 @@ __global__ __launch_bounds__(kCombineThreads) void flash_decode_combine_kernel(
             ms[u]       = -INFINITY;
             ls[u]       = 0.0f;
             os[u]       = f32x4{0.f, 0.f, 0.f, 0.f};
-            if (s < n_eff) {
+            if (s < num_splits) {
                 ms[u] = part_m[s];
                 ls[u] = part_l[s];
                 os[u] = *reinterpret_cast<const f32x4*>(&part_o[static_cast<int64_t>(s) * D + 4 * qd]);
             }
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const bool live = s0 + u * kGroups < n_eff;
+            ms[u]           = live ? ms[u] : -INFINITY;
+            ls[u]           = live ? ls[u] : 0.0f;
+            os[u]           = live ? os[u] : f32x4{0.f, 0.f, 0.f, 0.f};
         }
         float mx = m;
 #pragma unroll

@@ -191,7 +191,7 @@ __global__ __launch_bounds__(kPfThreads, 2) void flash_prefill_kernel(
     for (int i = 0; i < 4; ++i) {
         o[i] = f32x16{};
     }
-    float m_run = -INFINITY;
+    float m_ref = 0.0f;   // lazy reference maximum of this lane's row (log2 units)
     float l_run = 0.0f;
 
     PfRaw raw;
@@ -239,9 +239,9 @@ __global__ __launch_bounds__(kPfThreads, 2) void flash_prefill_kernel(
             __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
         }
 
-        // t = s * (k_scale * scale * log2 e) - m_ref, one fma per score.
-        // Register r of block kb is key 32kb + 8(r/4) + 4h + r%4 of the tile.
-        const float base = (m_run == -INFINITY) ? 0.0f : m_run;
+        // t = s * (k_scale * scale * log2 e) - m_ref, one fma per score, in
+        // place. Register r of block kb is key 32kb + 8(r/4) + 4h + r%4 of the
+        // tile.
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb) {
 #pragma unroll
@@ -249,7 +249,7 @@ __global__ __launch_bounds__(kPfThreads, 2) void flash_prefill_kernel(
                 const f32x4 kf = *reinterpret_cast<const f32x4*>(sKf + 32 * kb + 8 * rg + 4 * h);
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
-                    s[kb][4 * rg + e] = fmaf(s[kb][4 * rg + e], kf[e], -base);
+                    s[kb][4 * rg + e] = fmaf(s[kb][4 * rg + e], kf[e], -m_ref);
                 }
             }
         }
@@ -267,55 +267,64 @@ __global__ __launch_bounds__(kPfThreads, 2) void flash_prefill_kernel(
                 }
             }
         }
-        float tmax = -INFINITY;
+
+        // p = 2^t against the lazy reference maximum m_ref, the row sum of p
+        // and the P^T operands (p * v_scale rounded to bf16).
+        bf16x8 pop[4];
+        float  psum  = 0.0f;
+        auto   exp_p = [&]() {
+            psum = 0.0f;
 #pragma unroll
-        for (int kb = 0; kb < 2; ++kb) {
+            for (int kb = 0; kb < 2; ++kb) {
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                tmax = fmaxf(tmax, s[kb][r]);
+                for (int half = 0; half < 2; ++half) {
+                    u32x4 pw;
+#pragma unroll
+                    for (int rr = 0; rr < 2; ++rr) {
+                        const int   rg = 2 * half + rr;
+                        const f32x4 vf = *reinterpret_cast<const f32x4*>(sVf + 32 * kb + 8 * rg + 4 * h);
+                        const float p0 = __builtin_amdgcn_exp2f(s[kb][4 * rg + 0]);
+                        const float p1 = __builtin_amdgcn_exp2f(s[kb][4 * rg + 1]);
+                        const float p2 = __builtin_amdgcn_exp2f(s[kb][4 * rg + 2]);
+                        const float p3 = __builtin_amdgcn_exp2f(s[kb][4 * rg + 3]);
+                        psum += (p0 + p1) + (p2 + p3);
+                        pw[2 * rr]     = pack_bf16x2(p0 * vf[0], p1 * vf[1]);
+                        pw[2 * rr + 1] = pack_bf16x2(p2 * vf[2], p3 * vf[3]);
+                    }
+                    pop[2 * kb + half] = __builtin_bit_cast(bf16x8, pw);
+                }
             }
-        }
-        // Lazy reference max (exact): scores are exponentiated against m_run,
-        // raised only when one exceeds it by more than 2^8, so most tiles need
-        // no cross-lane step and no O rescale.
-        if (!__all((tmax <= 8.0f) && (m_run != -INFINITY))) {
+        };
+        exp_p();
+        // Lazy reference maximum (exact): m_ref moves to the row maximum only
+        // on the first tile or when a row sum exceeds 2^64 (some score more
+        // than 64 above m_ref); otherwise the tile needs no max reduction, no
+        // cross-lane step and no accumulator rescale. Every p and l use the
+        // same m_ref, and p <= 2^64 keeps l and O finite in fp32.
+        if (__any((kt == 0) || !(psum <= 0x1p64f))) {
+            float tmax = -INFINITY;
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb) {
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    tmax = fmaxf(tmax, s[kb][r]);
+                }
+            }
             tmax              = wave_xor_max(tmax, 32);
-            const float m_new = fmaxf(m_run, base + tmax);
-            const float delta = m_new - base;
-            const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+            const float delta = (tmax == -INFINITY) ? 0.0f : tmax;
+            // On the first tile l and O are still zero (and 2^-delta may be inf).
+            const float alpha = (kt == 0) ? 1.0f : __builtin_amdgcn_exp2f(-delta);
 #pragma unroll
             for (int kb = 0; kb < 2; ++kb) {
                 s[kb] -= delta;
             }
+            m_ref += delta;
             l_run *= alpha;
 #pragma unroll
             for (int db = 0; db < 4; ++db) {
                 o[db] *= alpha;
             }
-            m_run = m_new;
-        }
-
-        bf16x8 pop[4];
-        float  psum = 0.0f;
-#pragma unroll
-        for (int kb = 0; kb < 2; ++kb) {
-#pragma unroll
-            for (int half = 0; half < 2; ++half) {
-                u32x4 pw;
-#pragma unroll
-                for (int rr = 0; rr < 2; ++rr) {
-                    const int   rg   = 2 * half + rr;
-                    const f32x4 vf   = *reinterpret_cast<const f32x4*>(sVf + 32 * kb + 8 * rg + 4 * h);
-                    const float p0   = __builtin_amdgcn_exp2f(s[kb][4 * rg + 0]);
-                    const float p1   = __builtin_amdgcn_exp2f(s[kb][4 * rg + 1]);
-                    const float p2   = __builtin_amdgcn_exp2f(s[kb][4 * rg + 2]);
-                    const float p3   = __builtin_amdgcn_exp2f(s[kb][4 * rg + 3]);
-                    psum += (p0 + p1) + (p2 + p3);
-                    pw[2 * rr]     = pack_bf16x2(p0 * vf[0], p1 * vf[1]);
-                    pw[2 * rr + 1] = pack_bf16x2(p2 * vf[2], p3 * vf[3]);
-                }
-                pop[2 * kb + half] = __builtin_bit_cast(bf16x8, pw);
-            }
+            exp_p();
         }
         l_run += psum;
 

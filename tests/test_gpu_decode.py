@@ -139,3 +139,21 @@ def test_repeated_calls_share_scratch():
                                   hq, hkv, d, scale)
         sync()
         check(bf16_host(out), q, k8, v8, ks, vs, cl, hq, hkv, d, scale)
+
+
+@pytest.mark.parametrize("splits", [1, 4, 32])
+def test_score_dynamic_range(splits):
+    """Deep negative scores on the first keys and a far jump above the running
+    maximum at keys 400..404 (the split softmax must rescale exactly)."""
+    total, hq, hkv, d = 700, 8, 2, 128
+    scale = np.float32(1.0 / np.sqrt(d))
+    q = O.normal_bf16((hq, d), 41) & np.uint16(0x7FFF)
+    k8, ks = O.quantize_kv_fp8(O.normal_bf16((total * hkv, d), 42), d)
+    v8, vs = O.quantize_kv_fp8(O.normal_bf16((total * hkv, d), 43), d)
+    k8[: 64 * hkv] |= np.uint8(0x80)
+    ks[: 64 * hkv] = 0.5
+    k8[400 * hkv: 405 * hkv] &= np.uint8(0x7F)
+    ks[400 * hkv: 405 * hkv] = 0.05
+    got = gpu_decode(q, k8, v8, ks, vs, total - 1, hq, hkv, d, splits, scale)
+    assert np.isfinite(O.bf16_to_f32(got)).all()
+    check(got, q, k8, v8, ks, vs, total - 1, hq, hkv, d, scale)

@@ -48,6 +48,36 @@ def test_reference_cases(n_new, clen, hq, hkv, naive):
     assert mx <= MAX_ABS and mean <= MEAN_ABS, (mx, mean)
 
 
+def dynamic_range_inputs(n, hq, hkv, d):
+    """Scores that swing far in both directions: q >= 0; the first 64 keys
+    negative with a large scale (every row's first tile scores below -500 in
+    natural units); keys 400..404 positive with a large scale (a jump of ~50
+    above the running maximum mid-sequence); the rest ordinary."""
+    q = O.normal_bf16((n, hq, d), 31) & np.uint16(0x7FFF)
+    k8, ks = O.quantize_kv_fp8(O.normal_bf16((n * hkv, d), 32), d)
+    v8, vs = O.quantize_kv_fp8(O.normal_bf16((n * hkv, d), 33), d)
+    first = slice(0, 64 * hkv)
+    spike = slice(400 * hkv, 405 * hkv)
+    k8[first] |= np.uint8(0x80)
+    ks[first] = 0.5
+    k8[spike] &= np.uint8(0x7F)
+    ks[spike] = 0.05
+    return q, k8, v8, ks.astype(np.float32), vs
+
+
+def test_score_dynamic_range_rebases():
+    """The lazy reference maximum must rebase on the first tile (deep
+    negative scores) and again when a later score jumps far above it."""
+    n, hq, hkv, d = 700, 8, 2, 128
+    scale = np.float32(1.0 / np.sqrt(d))
+    q, k8, v8, ks, vs = dynamic_range_inputs(n, hq, hkv, d)
+    got = gpu_prefill(q, k8, v8, ks, vs, n, 0, hq, hkv, d, scale)
+    want = O.attention_f32(q, k8, v8, ks, vs, n, 0, hq, hkv, d, scale, NTHREADS)
+    assert np.isfinite(O.bf16_to_f32(got)).all()
+    mx, mean = O.bf16_err(got, want)
+    assert mx <= MAX_ABS and mean <= MEAN_ABS, (mx, mean)
+
+
 def rope_qkv(n, hq, hkv, d, theta, llama3, seed):
     q = O.normal_bf16((n, hq, d), seed)
     k = O.normal_bf16((n, hkv, d), seed + 1)
