@@ -366,7 +366,7 @@ def main() -> int:
         if args.sweep != "prefill":
             decode_kernel_sweep(torch, R, stream, [(24, 8, 35, None), (24, 8, 2041, None),
                                                    (24, 8, 8196, None), (24, 8, 32768, None),
-                                                   (32, 8, 131072, 64)])
+                                                   (32, 8, 131072, None), (32, 8, 131072, 64)])
         if args.sweep != "decode":
             prefill_sweep(torch, R, stream, [1021, 2048, 4096, 8192, 16384])
         return 0

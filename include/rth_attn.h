@@ -71,7 +71,9 @@ int rth_kv_append_fp8(uint8_t* k_cache, uint8_t* v_cache, float* k_scale,
 size_t rth_split_scratch_floats(int num_q_heads, int head_dim, int max_splits);
 
 /* Split count AdaptiveAttention uses on `device` for num_kv_heads kv heads:
- * enough (kv head, split) workgroups to fill every compute unit. */
+ * the decode kernel runs one wave per (kv head, split) unit, eight per
+ * compute unit, so this is 8 * CUs / num_kv_heads (256 for 8 kv heads on
+ * MI355X), capped at 1024. */
 int rth_default_num_splits(int num_kv_heads, int device);
 
 /* Replaces kernels::flash_decode_split_bf16 (reference

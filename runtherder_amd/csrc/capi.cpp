@@ -139,11 +139,10 @@ int rth_default_num_splits(int num_kv_heads, int device) {
     if (num_kv_heads < 1) {
         num_kv_heads = 1;
     }
-    // One 8-wave (kv head, split) workgroup per compute unit, rounded to a
-    // multiple of 8 splits so the XCD-aware mapping applies.
-    int s = (cus + num_kv_heads - 1) / num_kv_heads;
-    s     = (s + 7) / 8 * 8;
-    return s < 8 ? 8 : s;
+    // Decode runs one wave per (kv head, split) unit and eight of them per
+    // compute unit (two per SIMD), so one full wave of units is 8 * CUs.
+    int s = (8 * cus + num_kv_heads - 1) / num_kv_heads;
+    return s < 1 ? 1 : (s > 1024 ? 1024 : s);
 }
 
 int rth_attn_decode_split(uint16_t* out, const uint16_t* q, const uint8_t* k,

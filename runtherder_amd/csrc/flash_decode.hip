@@ -5,8 +5,8 @@
 // then a log-sum-exp merge of the splits, bf16 RNE output. The MI355X design
 // differs from the reference's one-block-per-q-head layout:
 //
-//  * One workgroup per (kv head, split) serves the whole GQA group, so every
-//    K/V byte is read from HBM once, not Hq/Hkv times.
+//  * One (kv head, split) unit serves the whole GQA group, so every K/V byte
+//    is read from HBM once, not Hq/Hkv times.
 //  * Scores and the value product run on bf16 MFMA (v_mfma_f32_16x16x32_bf16)
 //    with the GQA group as the 16-wide N dimension: S^T = K Q^T, then
 //    O^T += V^T P^T. E4M3 codes convert exactly to bf16 in registers
@@ -14,22 +14,31 @@
 //    in fp32 into the score column (k_scale) and into P (v_scale).
 //  * K is loaded with 16-byte lane loads along head_dim; V is loaded 8 bytes
 //    per (key, lane) and transposed in registers with v_perm so P^T needs no
-//    cross-lane movement.
+//    cross-lane movement. Each wave keeps a ring of two register tiles in
+//    flight.
 //  * Softmax runs in base 2 (scores pre-multiplied by scale*log2(e)); the
 //    running-max rescale of the accumulator is skipped when no lane's max
 //    moved.
-//  * Each workgroup writes its split's (m, l, O) partial; a second small
-//    kernel merges the splits of every q head with one round of loads (each
-//    thread folds a strided subset of splits, then the subsets merge in LDS).
-//    The scratch layout is the reference's ([Hq,S] m, [Hq,S] l,
-//    [Hq,S,D] acc); it needs no initialization.
-//  * Workgroups of one split for all kv heads land on one XCD, so the
-//    interleaved [token, kv_head] scale lines are fetched into one L2.
+//  * Two partitions, chosen on device from *cache_len:
+//      - long contexts (> kCoopMaxKeys keys): one WAVE per (kv head, split)
+//        unit, num_splits splits. A workgroup holds the kv heads of one
+//        split (its waves share the interleaved scale lines in L1); waves
+//        never wait for each other and each writes its own partial.
+//      - short contexts: one WORKGROUP per (kv head, split), the eight waves
+//        take alternate tiles and merge in LDS, so 8x fewer partials reach
+//        the merge kernel (whose launch and loads dominate at this size).
+//        Workgroups of one split for all kv heads land on one XCD.
+//  * A second small kernel merges the splits of every (q head, 32-wide d
+//    slice): one round of loads, an online max per thread over a strided
+//    subset of splits, then a tree merge in LDS. The scratch layout is the
+//    reference's ([Hq,S] m, [Hq,S] l, [Hq,S,D] acc); it needs no
+//    initialization.
 //
 // The key range of split si is [si*per, min(si*per+per, n_keys)) with
-// per = 32 * ceil(ceil(n_keys / S) / 32); splits past the last key exit at
-// once and the merge skips them. n_keys = *cache_len + 1 is read on device, so
-// one launch configuration serves every decode step (graph capturable).
+// per = 32 * ceil(ceil(n_keys / splits) / 32); splits past the last key exit
+// at once and the merge skips them. n_keys = *cache_len + 1 is read on
+// device, so one launch configuration serves every decode step (graph
+// capturable).
 #include "device_common.hpp"
 #include "launch.hpp"
 
@@ -39,8 +48,10 @@ namespace {
 constexpr int kDecWaves   = 8;
 constexpr int kDecThreads = kDecWaves * kWave;
 constexpr int kTileKeys   = 32;     // keys per wave iteration (two 16-key MFMAs)
-constexpr int kMaxGroupD  = 2048;   // G * head_dim bound of the LDS wave merge
+constexpr int kMaxGroupD  = 2048;   // G * head_dim bound of a wave's LDS partial staging
 constexpr int kCombineThreads = 256;
+constexpr int kCombineSlice   = 32;    // head_dim slice per merge workgroup
+constexpr int kCoopMaxKeys    = 4096;  // contexts up to this run cooperative workgroups
 
 template <int D>
 struct DecTraits {
@@ -108,6 +119,31 @@ __device__ __forceinline__ void load_tile(TileRaw<D>& t, const uint8_t* __restri
     }
 }
 
+// Partition of the decode work for one call. Long contexts run one wave per
+// (kv head, split) unit (num_splits splits, no merge inside a workgroup);
+// up to kCoopMaxKeys keys the eight waves of a workgroup share one
+// (kv head, split) key range and merge in LDS, which leaves 8x fewer partials
+// for the merge kernel (coop_splits splits). Both kernels derive the same
+// partition from *cache_len, so it is decided on device per call.
+struct DecPartition {
+    bool coop;
+    int  splits;   // partials per q head
+    int  per;      // keys per split (multiple of kTileKeys)
+    int  n_eff;    // splits holding at least one key
+};
+
+__device__ __forceinline__ DecPartition dec_partition(int n_keys, int num_splits, int hkv) {
+    DecPartition pt;
+    const int wgs         = (num_splits * hkv + kDecWaves - 1) / kDecWaves;
+    const int coop_splits = wgs / hkv;
+    pt.coop               = (n_keys <= kCoopMaxKeys) && (coop_splits >= 1);
+    pt.splits             = pt.coop ? coop_splits : num_splits;
+    int per               = (n_keys + pt.splits - 1) / pt.splits;
+    pt.per                = (per + kTileKeys - 1) & ~(kTileKeys - 1);
+    pt.n_eff              = (n_keys + pt.per - 1) / pt.per;
+    return pt;
+}
+
 template <int D>
 __global__ __launch_bounds__(kDecThreads) void flash_decode_kernel(
     const uint16_t* __restrict__ q, const uint8_t* __restrict__ k,
@@ -117,9 +153,9 @@ __global__ __launch_bounds__(kDecThreads) void flash_decode_kernel(
     using T = DecTraits<D>;
 
     __shared__ __attribute__((aligned(16))) float sm_sc[kDecWaves][64];
+    __shared__ __attribute__((aligned(16))) float sm_o[kDecWaves][kMaxGroupD];
     __shared__ float sm_m[kDecWaves][16];
     __shared__ float sm_l[kDecWaves][16];
-    __shared__ __attribute__((aligned(16))) float sm_o[kDecWaves * kMaxGroupD];
 
     const int G    = hq / hkv;
     const int tid  = static_cast<int>(threadIdx.x);
@@ -127,11 +163,21 @@ __global__ __launch_bounds__(kDecThreads) void flash_decode_kernel(
     const int lane = tid & (kWave - 1);
     const int n    = lane & 15;
     const int g    = lane >> 4;
+    const int bid  = static_cast<int>(blockIdx.x);
 
-    // XCD-aware block mapping: all kv heads of one split share bid % 8.
-    const int bid = static_cast<int>(blockIdx.x);
-    int       si, kvh;
-    if ((num_splits & 7) == 0) {
+    const int          n_keys = *cache_len + 1;
+    const DecPartition pt     = dec_partition(n_keys, num_splits, hkv);
+    // coop: workgroup = (kv head, split), waves take tiles wave, wave + 8, ...
+    // solo: wave = (kv head, split) unit; adjacent units are the kv heads of
+    //       one split, so a workgroup's waves share the scale lines in L1.
+    int kvh, si;
+    if (!pt.coop) {
+        const int unit = bid * kDecWaves + wave;
+        kvh            = unit % hkv;
+        si             = unit / hkv;
+    } else if ((pt.splits & 7) == 0) {
+        // All kv heads of one split on one XCD (bid % 8), so the interleaved
+        // [token, kv_head] K/V rows and scale lines are fetched into one L2.
         const int r = bid >> 3;
         si          = (r / hkv) * 8 + (bid & 7);
         kvh         = r % hkv;
@@ -139,9 +185,16 @@ __global__ __launch_bounds__(kDecThreads) void flash_decode_kernel(
         si  = bid / hkv;
         kvh = bid % hkv;
     }
+    if (si >= pt.n_eff) {   // uniform per workgroup in coop mode
+        return;
+    }
+    const int k0      = si * pt.per;
+    const int k1      = min(k0 + pt.per, n_keys);
+    const int n_tiles = (k1 - k0 + kTileKeys - 1) / kTileKeys;
+    const int t_first = pt.coop ? wave : 0;
+    const int t_step  = pt.coop ? kDecWaves : 1;
 
     // Q^T as the B operand: column n = q head of the group (zero past G).
-    // Loaded before cache_len is known, so both loads are in flight together.
     bf16x8 qop[T::kKSteps];
     {
         const bool      has = n < G;
@@ -158,17 +211,6 @@ __global__ __launch_bounds__(kDecThreads) void flash_decode_kernel(
             }
         }
     }
-
-    const int n_keys = *cache_len + 1;
-    int       per    = (n_keys + num_splits - 1) / num_splits;
-    per              = (per + kTileKeys - 1) & ~(kTileKeys - 1);
-    const int n_eff  = (n_keys + per - 1) / per;
-    if (si >= n_eff) {
-        return;
-    }
-    const int k0      = si * per;
-    const int k1      = min(k0 + per, n_keys);
-    const int n_tiles = (k1 - k0 + kTileKeys - 1) / kTileKeys;
 
     f32x4 oacc[T::kOMfma];
 #pragma unroll
@@ -275,32 +317,32 @@ __global__ __launch_bounds__(kDecThreads) void flash_decode_kernel(
         __builtin_amdgcn_wave_barrier();
     };
 
-    // Ring of kRing register tiles: the load of tile i + kRing - 1 is issued
-    // before tile i is consumed, with compile-time buffer indices and no
-    // branch in between, so kRing - 1 tiles stay in flight per wave while it
-    // computes (the memory latency under full load is several microseconds).
-    // Tile indices past the split's last tile are clamped to it; those
-    // reloads hit in L2 and are never consumed.
+    // Ring of kRing register tiles: the load of the tile kRing - 1 steps ahead
+    // is issued before the current tile is consumed, with compile-time
+    // buffer indices and no branch in between, so kRing - 1 tiles stay in
+    // flight per wave while it computes. Tile indices past this wave's last
+    // tile are clamped to it; those reloads hit in L2 and are never consumed.
     constexpr int kRing     = DecTraits<D>::kRing;
     const int     last_tile = n_tiles - 1;
-    if (wave <= last_tile) {
+    if (t_first <= last_tile) {
         TileRaw<D> ring[kRing];
 #pragma unroll
         for (int r = 0; r + 1 < kRing; ++r) {
-            load_tile<D>(ring[r], k, v, ks, vs, k0 + min(wave + r * kDecWaves, last_tile) * kTileKeys,
-                         k1, kvh, hkv, lane);
+            load_tile<D>(ring[r], k, v, ks, vs,
+                         k0 + min(t_first + r * t_step, last_tile) * kTileKeys, k1, kvh, hkv,
+                         lane);
         }
-        for (int t = wave;; t += kRing * kDecWaves) {
+        for (int t = t_first;; t += kRing * t_step) {
             bool done = false;
 #pragma unroll
             for (int r = 0; r < kRing; ++r) {
                 if (!done) {
-                    const int tr = t + r * kDecWaves;
+                    const int tr = t + r * t_step;
                     load_tile<D>(ring[(r + kRing - 1) % kRing], k, v, ks, vs,
-                                 k0 + min(tr + (kRing - 1) * kDecWaves, last_tile) * kTileKeys,
+                                 k0 + min(tr + (kRing - 1) * t_step, last_tile) * kTileKeys,
                                  k1, kvh, hkv, lane);
                     process(ring[r], k0 + tr * kTileKeys);
-                    done = tr + kDecWaves > last_tile;
+                    done = tr + t_step > last_tile;
                 }
             }
             if (done) {
@@ -309,101 +351,124 @@ __global__ __launch_bounds__(kDecThreads) void flash_decode_kernel(
         }
     }
 
-    // ---- merge the waves of this workgroup --------------------------------
+    // ---- partial of this split, reference layout: m at [h*S + si] (log2
+    // units), l at [Hq*S + h*S + si], acc at [2*Hq*S + (h*S + si)*D + d]
+    // with S = num_splits (coop mode fills the first pt.splits slots).
     l_run = wave_xor_sum(l_run, 16);
     l_run = wave_xor_sum(l_run, 32);
-    if (g == 0) {
-        sm_m[wave][n] = m_run;
-        sm_l[wave][n] = l_run;
-    }
-    __syncthreads();
-    float wf = 0.0f;  // this lane's head: factor of this wave against the block max
-    if (n < G) {
-        float M = -INFINITY;
-#pragma unroll
-        for (int w = 0; w < kDecWaves; ++w) {
-            M = fmaxf(M, sm_m[w][n]);
-        }
-        wf = (m_run == -INFINITY) ? 0.0f : exp2f(m_run - M);
-#pragma unroll
-        for (int c = 0; c < T::kOMfma; ++c) {
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int d = T::kVBytes * (4 * g + r) + c;
-                sm_o[(wave * G + n) * D + d] = oacc[c][r] * wf;
-            }
-        }
-    }
-    __syncthreads();
-
-    // Partial of this split, reference layout: m at [h*S + si] (log2 units),
-    // l at [Hq*S + h*S + si], acc at [2*Hq*S + (h*S + si)*D + d].
     const int64_t hs     = static_cast<int64_t>(hq) * num_splits;
     float*        part_m = partial;
     float*        part_l = partial + hs;
     float*        part_o = partial + 2 * hs;
-    for (int e = tid; e < G * (D / 4); e += kDecThreads) {
-        const int h  = e / (D / 4);
-        const int d0 = 4 * (e - h * (D / 4));
-        f32x4     a  = {0.f, 0.f, 0.f, 0.f};
+    if (pt.coop) {
+        // Merge the eight waves: each scales its O^T by 2^(m_w - M) into its
+        // LDS rows, then the rows are summed along d.
+        if (g == 0) {
+            sm_m[wave][n] = m_run;
+            sm_l[wave][n] = l_run;
+        }
+        __syncthreads();
+        if (n < G) {
+            float M = -INFINITY;
 #pragma unroll
-        for (int w = 0; w < kDecWaves; ++w) {
-            a += *reinterpret_cast<const f32x4*>(&sm_o[(w * G + h) * D + d0]);
+            for (int w = 0; w < kDecWaves; ++w) {
+                M = fmaxf(M, sm_m[w][n]);
+            }
+            const float wf = (m_run == -INFINITY) ? 0.0f : exp2f(m_run - M);
+#pragma unroll
+            for (int c = 0; c < T::kOMfma; ++c) {
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    sm_o[wave][n * D + T::kVBytes * (4 * g + r) + c] = oacc[c][r] * wf;
+                }
+            }
         }
-        const int64_t slot = static_cast<int64_t>(kvh * G + h) * num_splits + si;
-        *reinterpret_cast<f32x4*>(&part_o[slot * D + d0]) = a;
-    }
-    if (tid < G) {
-        float M = -INFINITY;
-        for (int w = 0; w < kDecWaves; ++w) {
-            M = fmaxf(M, sm_m[w][tid]);
+        __syncthreads();
+        for (int e = tid; e < G * (D / 4); e += kDecThreads) {
+            const int h  = e / (D / 4);
+            const int d0 = 4 * (e - h * (D / 4));
+            f32x4     a  = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int w = 0; w < kDecWaves; ++w) {
+                a += *reinterpret_cast<const f32x4*>(&sm_o[w][h * D + d0]);
+            }
+            const int64_t slot = static_cast<int64_t>(kvh * G + h) * num_splits + si;
+            *reinterpret_cast<f32x4*>(&part_o[slot * D + d0]) = a;
         }
-        float L = 0.0f;
-        for (int w = 0; w < kDecWaves; ++w) {
-            const float mw = sm_m[w][tid];
-            L += (mw == -INFINITY) ? 0.0f : sm_l[w][tid] * exp2f(mw - M);
+        if (tid < G) {
+            float M = -INFINITY;
+            for (int w = 0; w < kDecWaves; ++w) {
+                M = fmaxf(M, sm_m[w][tid]);
+            }
+            float L = 0.0f;
+            for (int w = 0; w < kDecWaves; ++w) {
+                const float mw = sm_m[w][tid];
+                L += (mw == -INFINITY) ? 0.0f : sm_l[w][tid] * exp2f(mw - M);
+            }
+            const int64_t slot = static_cast<int64_t>(kvh * G + tid) * num_splits + si;
+            part_m[slot]       = M;
+            part_l[slot]       = L;
         }
-        const int64_t slot = static_cast<int64_t>(kvh * G + tid) * num_splits + si;
-        part_m[slot]       = M;
-        part_l[slot]       = L;
+    } else {
+        // O^T goes through this wave's LDS rows so the stores run along d.
+        float* so = sm_o[wave];
+        if (n < G) {
+#pragma unroll
+            for (int c = 0; c < T::kOMfma; ++c) {
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    so[n * D + T::kVBytes * (4 * g + r) + c] = oacc[c][r];
+                }
+            }
+        }
+        __builtin_amdgcn_wave_barrier();
+        for (int e = lane; e < G * (D / 4); e += kWave) {
+            const int     h    = e / (D / 4);
+            const int     d0   = 4 * (e - h * (D / 4));
+            const int64_t slot = static_cast<int64_t>(kvh * G + h) * num_splits + si;
+            *reinterpret_cast<f32x4*>(&part_o[slot * D + d0]) =
+                *reinterpret_cast<const f32x4*>(&so[h * D + d0]);
+        }
+        if (g == 0 && n < G) {
+            const int64_t slot = static_cast<int64_t>(kvh * G + n) * num_splits + si;
+            part_m[slot]       = m_run;
+            part_l[slot]       = l_run;
+        }
     }
 }
 
-// One workgroup per q head: merges the n_eff split partials,
-// out = sum_s 2^(m_s - M) acc_s / sum_s 2^(m_s - M) l_s (reference
-// src/kernels/flash_decode.cu:222-247). Thread (group g, quad q) folds
-// splits g, g + kGroups, ... for d = 4q .. 4q+3 with an online max, so every
-// load is issued up front; the kGroups states merge through LDS.
+// One workgroup per (q head, 32-wide slice of head_dim): merges the n_eff
+// split partials, out = sum_s 2^(m_s - M) acc_s / sum_s 2^(m_s - M) l_s
+// (reference src/kernels/flash_decode.cu:222-247). Thread (group grp, quad
+// qd) folds splits grp, grp + kGroups, ... for d = 4qd .. 4qd+3 of the slice
+// with an online max, eight loads in flight at a time; the kGroups states
+// merge through LDS.
 template <int D>
 __global__ __launch_bounds__(kCombineThreads) void flash_decode_combine_kernel(
     uint16_t* __restrict__ out, const float* __restrict__ partial, int num_splits,
-    const int* __restrict__ cache_len, int hq) {
-    constexpr int kQuads  = D / 4;
+    const int* __restrict__ cache_len, int hq, int hkv) {
+    constexpr int kQuads  = kCombineSlice / 4;
     constexpr int kGroups = kCombineThreads / kQuads;
     __shared__ __attribute__((aligned(16))) f32x4 sm_acc[kGroups][kQuads];
     __shared__ float sm_mm[kGroups], sm_ll[kGroups];
 
     const int qh  = static_cast<int>(blockIdx.x);
+    const int dsl = static_cast<int>(blockIdx.y) * kCombineSlice;
     const int tid = static_cast<int>(threadIdx.x);
     const int grp = tid / kQuads;
     const int qd  = tid - grp * kQuads;
 
     const int n_keys = *cache_len + 1;
-    int       per    = (n_keys + num_splits - 1) / num_splits;
-    per              = (per + kTileKeys - 1) & ~(kTileKeys - 1);
-    const int n_eff  = (n_keys + per - 1) / per;
+    const int n_eff  = dec_partition(n_keys, num_splits, hkv).n_eff;
 
     const int64_t hs     = static_cast<int64_t>(hq) * num_splits;
     const float*  part_m = partial + static_cast<int64_t>(qh) * num_splits;
     const float*  part_l = partial + hs + static_cast<int64_t>(qh) * num_splits;
-    const float*  part_o = partial + 2 * hs + static_cast<int64_t>(qh) * num_splits * D;
+    const float*  part_o = partial + 2 * hs + static_cast<int64_t>(qh) * num_splits * D + dsl;
 
     float m = -INFINITY, l = 0.0f;
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-    // Slots are loaded up to num_splits, in flight with the cache_len load;
-    // slots at or past n_eff hold stale data and are replaced by selects (not
-    // multiplied by zero, which would keep a stale NaN).
-    for (int s0 = grp; s0 < num_splits; s0 += 8 * kGroups) {
+    for (int s0 = grp; s0 < n_eff; s0 += 8 * kGroups) {
         float ms[8], ls[8];
         f32x4 os[8];
 #pragma unroll
@@ -412,18 +477,11 @@ __global__ __launch_bounds__(kCombineThreads) void flash_decode_combine_kernel(
             ms[u]       = -INFINITY;
             ls[u]       = 0.0f;
             os[u]       = f32x4{0.f, 0.f, 0.f, 0.f};
-            if (s < num_splits) {
+            if (s < n_eff) {
                 ms[u] = part_m[s];
                 ls[u] = part_l[s];
                 os[u] = *reinterpret_cast<const f32x4*>(&part_o[static_cast<int64_t>(s) * D + 4 * qd]);
             }
-        }
-#pragma unroll
-        for (int u = 0; u < 8; ++u) {
-            const bool live = s0 + u * kGroups < n_eff;
-            ms[u]           = live ? ms[u] : -INFINITY;
-            ls[u]           = live ? ls[u] : 0.0f;
-            os[u]           = live ? os[u] : f32x4{0.f, 0.f, 0.f, 0.f};
         }
         float mx = m;
 #pragma unroll
@@ -441,31 +499,35 @@ __global__ __launch_bounds__(kCombineThreads) void flash_decode_combine_kernel(
         }
         m = mx;
     }
-    if (qd == 0) {
-        sm_mm[grp] = m;
-        sm_ll[grp] = l;
+    // Tree merge of the kGroups states: at each level the upper half of the
+    // groups hands its state to the lower half through LDS.
+#pragma unroll
+    for (int stride = kGroups / 2; stride >= 1; stride /= 2) {
+        if (grp >= stride && grp < 2 * stride) {
+            sm_acc[grp - stride][qd] = acc;
+            if (qd == 0) {
+                sm_mm[grp - stride] = m;
+                sm_ll[grp - stride] = l;
+            }
+        }
+        __syncthreads();
+        if (grp < stride) {
+            const float m2 = sm_mm[grp];
+            const float M  = fmaxf(m, m2);
+            const float f1 = (m == -INFINITY) ? 0.0f : exp2f(m - M);
+            const float f2 = (m2 == -INFINITY) ? 0.0f : exp2f(m2 - M);
+            acc            = acc * f1 + sm_acc[grp][qd] * f2;
+            l              = l * f1 + sm_ll[grp] * f2;
+            m              = M;
+        }
+        __syncthreads();
     }
-    sm_acc[grp][qd] = acc;
-    __syncthreads();
     if (grp == 0) {
-        float M = -INFINITY;
-#pragma unroll
-        for (int g2 = 0; g2 < kGroups; ++g2) {
-            M = fmaxf(M, sm_mm[g2]);
-        }
-        f32x4 t = {0.f, 0.f, 0.f, 0.f};
-        float L = 0.0f;
-#pragma unroll
-        for (int g2 = 0; g2 < kGroups; ++g2) {
-            const float f = (sm_mm[g2] == -INFINITY) ? 0.0f : exp2f(sm_mm[g2] - M);
-            t += sm_acc[g2][qd] * f;
-            L += sm_ll[g2] * f;
-        }
-        const float inv = 1.0f / L;
+        const float inv = 1.0f / l;
         u32x2       w2;
-        w2.x = pack_bf16x2(t[0] * inv, t[1] * inv);
-        w2.y = pack_bf16x2(t[2] * inv, t[3] * inv);
-        *reinterpret_cast<u32x2*>(out + static_cast<int64_t>(qh) * D + 4 * qd) = w2;
+        w2.x = pack_bf16x2(acc[0] * inv, acc[1] * inv);
+        w2.y = pack_bf16x2(acc[2] * inv, acc[3] * inv);
+        *reinterpret_cast<u32x2*>(out + static_cast<int64_t>(qh) * D + dsl + 4 * qd) = w2;
     }
 }
 
@@ -480,7 +542,8 @@ hipError_t launch_decode(uint16_t* out, const uint16_t* q, const uint8_t* k,
                          const uint8_t* v, const float* ks, const float* vs,
                          float* partial, int num_splits, const int* cache_len,
                          int hq, int hkv, float scale, hipStream_t stream) {
-    const dim3 grid(static_cast<unsigned>(num_splits * hkv));
+    const int  units = num_splits * hkv;
+    const dim3 grid(static_cast<unsigned>((units + kDecWaves - 1) / kDecWaves));
     hipLaunchKernelGGL(flash_decode_kernel<D>, grid, dim3(kDecThreads), 0, stream,
                        q, k, v, ks, vs, partial, num_splits, cache_len, hq, hkv,
                        scale * kLog2e);
@@ -488,9 +551,10 @@ hipError_t launch_decode(uint16_t* out, const uint16_t* q, const uint8_t* k,
     if (e != hipSuccess) {
         return e;
     }
-    hipLaunchKernelGGL(flash_decode_combine_kernel<D>, dim3(static_cast<unsigned>(hq)),
+    hipLaunchKernelGGL(flash_decode_combine_kernel<D>,
+                       dim3(static_cast<unsigned>(hq), static_cast<unsigned>(D / kCombineSlice)),
                        dim3(kCombineThreads), 0, stream, out, partial, num_splits,
-                       cache_len, hq);
+                       cache_len, hq, hkv);
     return hipGetLastError();
 }
 
