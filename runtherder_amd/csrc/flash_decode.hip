@@ -52,6 +52,7 @@ constexpr int kMaxGroupD  = 2048;   // G * head_dim bound of a wave's LDS partia
 constexpr int kCombineThreads = 256;
 constexpr int kCombineSlice   = 32;    // head_dim slice per merge workgroup
 constexpr int kCoopMaxKeys    = 4096;  // contexts up to this run cooperative workgroups
+constexpr int kWideUnits      = 1024;  // fewer (kv head, split) units: one workgroup each
 
 template <int D>
 struct DecTraits {
@@ -119,12 +120,15 @@ __device__ __forceinline__ void load_tile(TileRaw<D>& t, const uint8_t* __restri
     }
 }
 
-// Partition of the decode work for one call. Long contexts run one wave per
-// (kv head, split) unit (num_splits splits, no merge inside a workgroup);
-// up to kCoopMaxKeys keys the eight waves of a workgroup share one
-// (kv head, split) key range and merge in LDS, which leaves 8x fewer partials
-// for the merge kernel (coop_splits splits). Both kernels derive the same
-// partition from *cache_len, so it is decided on device per call.
+// Partition of the decode work for one call. With few units
+// (num_splits * hkv < kWideUnits) the host launches one workgroup per
+// (kv head, split) and the eight waves of a workgroup share its key range,
+// merging in LDS ("coop"). Otherwise it launches one wave per unit, eight per
+// workgroup; then long contexts run one wave per (kv head, split) unit
+// (num_splits splits, no merge inside a workgroup) and contexts up to
+// kCoopMaxKeys switch to coop over n_wgs / hkv splits, which leaves 8x fewer
+// partials for the merge kernel. Both kernels derive the same partition from
+// *cache_len and the launch shape, so it is decided on device per call.
 struct DecPartition {
     bool coop;
     int  splits;   // partials per q head
@@ -132,16 +136,22 @@ struct DecPartition {
     int  n_eff;    // splits holding at least one key
 };
 
-__device__ __forceinline__ DecPartition dec_partition(int n_keys, int num_splits, int hkv) {
+__device__ __forceinline__ DecPartition dec_partition(int n_keys, int num_splits, int hkv,
+                                                      int n_wgs) {
     DecPartition pt;
-    const int wgs         = (num_splits * hkv + kDecWaves - 1) / kDecWaves;
-    const int coop_splits = wgs / hkv;
-    pt.coop               = (n_keys <= kCoopMaxKeys) && (coop_splits >= 1);
+    const int coop_splits = n_wgs / hkv;
+    const bool wide       = n_wgs >= num_splits * hkv;
+    pt.coop               = wide || ((n_keys <= kCoopMaxKeys) && (coop_splits >= 1));
     pt.splits             = pt.coop ? coop_splits : num_splits;
     int per               = (n_keys + pt.splits - 1) / pt.splits;
     pt.per                = (per + kTileKeys - 1) & ~(kTileKeys - 1);
     pt.n_eff              = (n_keys + pt.per - 1) / pt.per;
     return pt;
+}
+
+__host__ __device__ constexpr int dec_workgroups(int num_splits, int hkv) {
+    return (num_splits * hkv < kWideUnits) ? num_splits * hkv
+                                           : (num_splits * hkv + kDecWaves - 1) / kDecWaves;
 }
 
 template <int D>
@@ -166,7 +176,8 @@ __global__ __launch_bounds__(kDecThreads) void flash_decode_kernel(
     const int bid  = static_cast<int>(blockIdx.x);
 
     const int          n_keys = *cache_len + 1;
-    const DecPartition pt     = dec_partition(n_keys, num_splits, hkv);
+    const DecPartition pt     = dec_partition(n_keys, num_splits, hkv,
+                                              static_cast<int>(gridDim.x));
     // coop: workgroup = (kv head, split), waves take tiles wave, wave + 8, ...
     // solo: wave = (kv head, split) unit; adjacent units are the kv heads of
     //       one split, so a workgroup's waves share the scale lines in L1.
@@ -446,7 +457,7 @@ __global__ __launch_bounds__(kDecThreads) void flash_decode_kernel(
 template <int D>
 __global__ __launch_bounds__(kCombineThreads) void flash_decode_combine_kernel(
     uint16_t* __restrict__ out, const float* __restrict__ partial, int num_splits,
-    const int* __restrict__ cache_len, int hq, int hkv) {
+    const int* __restrict__ cache_len, int hq, int hkv, int n_wgs) {
     constexpr int kQuads  = kCombineSlice / 4;
     constexpr int kGroups = kCombineThreads / kQuads;
     __shared__ __attribute__((aligned(16))) f32x4 sm_acc[kGroups][kQuads];
@@ -459,7 +470,7 @@ __global__ __launch_bounds__(kCombineThreads) void flash_decode_combine_kernel(
     const int qd  = tid - grp * kQuads;
 
     const int n_keys = *cache_len + 1;
-    const int n_eff  = dec_partition(n_keys, num_splits, hkv).n_eff;
+    const int n_eff  = dec_partition(n_keys, num_splits, hkv, n_wgs).n_eff;
 
     const int64_t hs     = static_cast<int64_t>(hq) * num_splits;
     const float*  part_m = partial + static_cast<int64_t>(qh) * num_splits;
@@ -542,8 +553,8 @@ hipError_t launch_decode(uint16_t* out, const uint16_t* q, const uint8_t* k,
                          const uint8_t* v, const float* ks, const float* vs,
                          float* partial, int num_splits, const int* cache_len,
                          int hq, int hkv, float scale, hipStream_t stream) {
-    const int  units = num_splits * hkv;
-    const dim3 grid(static_cast<unsigned>((units + kDecWaves - 1) / kDecWaves));
+    const int  n_wgs = dec_workgroups(num_splits, hkv);
+    const dim3 grid(static_cast<unsigned>(n_wgs));
     hipLaunchKernelGGL(flash_decode_kernel<D>, grid, dim3(kDecThreads), 0, stream,
                        q, k, v, ks, vs, partial, num_splits, cache_len, hq, hkv,
                        scale * kLog2e);
@@ -554,7 +565,7 @@ hipError_t launch_decode(uint16_t* out, const uint16_t* q, const uint8_t* k,
     hipLaunchKernelGGL(flash_decode_combine_kernel<D>,
                        dim3(static_cast<unsigned>(hq), static_cast<unsigned>(D / kCombineSlice)),
                        dim3(kCombineThreads), 0, stream, out, partial, num_splits,
-                       cache_len, hq, hkv);
+                       cache_len, hq, hkv, n_wgs);
     return hipGetLastError();
 }
 
