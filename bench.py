@@ -186,6 +186,43 @@ def bench_prefill(torch, R, stream, n=4096, iters=10):
             "append_gbs": app_bytes / (app_us * 1e-6) / 1e9}
 
 
+def bench_rope_append(torch, R, stream, n=4096, iters=20):
+    """Config-4 shapes (32Q/8KV, head_dim 128): RoPE on q and k then the K/V
+    append as two launches (rope_bf16 + append, the reference's sequence)
+    against the fused entry; algorithmic bytes of the fused call: q read and
+    written, k and v read, E4M3 codes and scales written."""
+    hq, hkv, d = 32, 8, 128
+    dev = torch.device("cuda:0")
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(99)
+    cache = R.KVCache(1, n, hkv, d, device=dev)
+    pos = torch.zeros(1, dtype=torch.int32, device=dev)
+    positions = torch.arange(n, dtype=torch.int32, device=dev)
+    inv = (1e6 ** (-torch.arange(0, d, 2, dtype=torch.float64, device=dev) / d)).float()
+    with torch.cuda.stream(stream):
+        q = torch.randn((n, hq, d), generator=gen, device=dev).to(torch.bfloat16)
+        k = torch.randn((n, hkv, d), generator=gen, device=dev).to(torch.bfloat16)
+        v = torch.randn((n, hkv, d), generator=gen, device=dev).to(torch.bfloat16)
+        for _ in range(2):
+            R.rope_bf16(q, k, positions, inv, n, hq, hkv, d)
+            cache.append(0, k, v, n, pos)
+            cache.append_rope(0, q, k, v, n, positions, inv, pos, hq)
+        torch.cuda.synchronize()
+        with EventTimer(torch, stream) as t2:
+            for _ in range(iters):
+                R.rope_bf16(q, k, positions, inv, n, hq, hkv, d)
+                cache.append(0, k, v, n, pos)
+        with EventTimer(torch, stream) as t1:
+            for _ in range(iters):
+                cache.append_rope(0, q, k, v, n, positions, inv, pos, hq)
+    torch.cuda.synchronize()
+    fused_bytes = n * hq * d * 4 + n * hkv * d * 4 + n * hkv * d * 2 + n * hkv * 8
+    us1, us2 = t1.ms * 1e3 / iters, t2.ms * 1e3 / iters
+    return {"n": n, "fused_us": round(us1, 2), "two_step_us": round(us2, 2),
+            "fused_gbs": round(fused_bytes / (us1 * 1e-6) / 1e9, 1),
+            "fused_bytes": fused_bytes}
+
+
 def decode_kernel_sweep(torch, R, stream, points):
     """Per-call decode time (split kernel + merge kernel) at several context
     depths, rotating over enough layers that the working set exceeds the
@@ -372,6 +409,7 @@ def main() -> int:
         return 0
     dec = bench_decode(torch, R, args, stream)
     pf = bench_prefill(torch, R, stream, n=args.prefill_n)
+    ra = bench_rope_append(torch, R, stream, n=args.prefill_n)
     cpu = None if args.no_cpu else cpu_baseline(torch, dec)
 
     line = {
@@ -412,6 +450,8 @@ def main() -> int:
                          "flops_per_launch": pf["flops"]},
             "append_us": round(pf["append_us"], 2), "append_gbs": round(pf["append_gbs"], 1),
         },
+        "rope_append": dict(ra, workload="config4 shapes: RoPE(q,k) + K/V FP8 append, fused "
+                                         "entry vs rope_bf16 then append"),
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

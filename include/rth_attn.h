@@ -115,6 +115,30 @@ int rth_attn_naive(uint16_t* out, const uint16_t* q, const uint8_t* k,
  * several decode steps. */
 int rth_advance_position(int* pos, int delta, void* stream);
 
+/* Replaces kernels::rope_bf16 (reference include/runtherder/kernels/
+ * rope.cuh:16-25): in-place rotate-half RoPE on q [seq_len, Hq, D] and
+ * k [seq_len, Hkv, D] bf16; token t rotates by positions[t] (device array)
+ * with inv_freq [D/2] (device). head_dim even, <= 256. sin/cos are taken in
+ * double precision of the fp32 angle, rounded to fp32. */
+int rth_rope_bf16(uint16_t* q, uint16_t* k, const int* positions,
+                  const float* inv_freq, int seq_len, int num_q_heads,
+                  int num_kv_heads, int head_dim, void* stream);
+
+/* No counterpart in the reference: fuses the caller sequence
+ * rope_bf16(q, k) then KVCache::append(layer, k, v, n_new, at_pos)
+ * (reference src/model/supported/llama/llama3.cu:228-232) into one launch.
+ * q is rotated in place exactly as rth_rope_bf16 does; rotated K and V rows
+ * are quantized into the layer's cache slabs at rows *at_pos .. *at_pos +
+ * n_new - 1, byte-identical to rth_rope_bf16 followed by rth_kv_append_fp8.
+ * The k input is read only (left unrotated, unlike the two-step sequence).
+ * head_dim in {64, 128, 256}. */
+int rth_rope_append_fp8(uint16_t* q, uint8_t* k_cache, uint8_t* v_cache,
+                        float* k_scale, float* v_scale, const uint16_t* k,
+                        const uint16_t* v, const int* positions,
+                        const float* inv_freq, const int* at_pos, int n_new,
+                        int num_q_heads, int num_kv_heads, int head_dim,
+                        void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -718,8 +718,11 @@ void rth_ref_rope_inv_freq_llama3(float* inv_freq, int head_dim,
 
 /* Rotate-half RoPE in place on x[n_tokens, num_heads, head_dim] bf16:
  * theta = float(pos) * inv_freq[i], (a, b) -> (a c - b s, a s + b c) for the
- * pair (i, i + D/2), each rounded to bf16 (src/kernels/rope.cu:32-54). Uses
- * sinf/cosf where the reference uses __sincosf. */
+ * pair (i, i + D/2), each rounded to bf16 (src/kernels/rope.cu:32-54), with
+ * the products grouped as fma(a, c, -(b s)) and fma(a, s, b c). sin and cos
+ * are taken in double of the fp32 angle and rounded to fp32 (the reference
+ * uses the __sincosf approximation; its test bound is max-abs 5e-2 against
+ * double, include/runtherder/kernels/rope.cuh:14). */
 void rth_ref_rope_apply_bf16(uint16_t* x, const int* positions,
                              const float* inv_freq, int n_tokens,
                              int num_heads, int head_dim) {
@@ -729,8 +732,8 @@ void rth_ref_rope_apply_bf16(uint16_t* x, const int* positions,
             uint16_t* row = x + ((int64_t)t * num_heads + h) * head_dim;
             for (int i = 0; i < half; ++i) {
                 const float th = (float)positions[t] * inv_freq[i];
-                const float s  = sinf(th);
-                const float c  = cosf(th);
+                const float s  = (float)sin((double)th);
+                const float c  = (float)cos((double)th);
                 const float a  = rth_ref_bf16_to_f32(row[i]);
                 const float b  = rth_ref_bf16_to_f32(row[i + half]);
                 row[i]         = rth_ref_f32_to_bf16(fmaf(a, c, -(b * s)));

@@ -25,6 +25,8 @@ from .ops import (  # noqa: F401
     new_flash_split_scratch,
     quantize_kv_fp8,
     quantize_kv_fp8_scaled,
+    rope_append_fp8,
+    rope_bf16,
 )
 
 LIB_PATH = _ffi.LIB_PATH

@@ -28,6 +28,9 @@ _SIGNATURES = {
     "rth_attn_naive": (_c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _c_int, _vp,
                                 _c_int, _c_int, _c_int, ctypes.c_float, _vp]),
     "rth_advance_position": (_c_int, [_vp, _c_int, _vp]),
+    "rth_rope_bf16": (_c_int, [_vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, _c_int, _vp]),
+    "rth_rope_append_fp8": (_c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
+                                     _c_int, _c_int, _c_int, _c_int, _vp]),
 }
 
 _lib: ctypes.CDLL | None = None

@@ -41,6 +41,7 @@ KERNEL_SOURCES = [
     "flash_decode.hip",
     "flash_prefill.hip",
     "attention_naive.hip",
+    "rope.hip",
     "capi.cpp",
 ]
 HOST_SOURCES = ["attention_backends.cpp"]

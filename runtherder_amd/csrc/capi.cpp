@@ -213,6 +213,47 @@ int rth_attn_naive(uint16_t* out, const uint16_t* q, const uint8_t* k,
                      "rth_attn_naive");
 }
 
+int rth_rope_bf16(uint16_t* q, uint16_t* k, const int* positions, const float* inv_freq,
+                  int seq_len, int num_q_heads, int num_kv_heads, int head_dim,
+                  void* stream) {
+    // Checks of rope_bf16 (reference src/kernels/rope.cu:68-73).
+    RTH_REQUIRE(q != nullptr && k != nullptr, "q and k must not be null");
+    RTH_REQUIRE(positions != nullptr && inv_freq != nullptr,
+                "positions and inv_freq must not be null");
+    RTH_REQUIRE(seq_len >= 1, "seq_len must be >= 1");
+    RTH_REQUIRE(num_q_heads >= 1, "num_q_heads must be >= 1");
+    RTH_REQUIRE(num_kv_heads >= 1, "num_kv_heads must be >= 1");
+    RTH_REQUIRE(head_dim >= 2, "head_dim must be >= 2");
+    RTH_REQUIRE(head_dim % 2 == 0, "head_dim must be even");
+    RTH_REQUIRE(head_dim <= 256, "head_dim exceeds kMaxHeadDim (256)");
+    return check_hip(rth::rope_bf16_launch(q, k, positions, inv_freq, seq_len, num_q_heads,
+                                           num_kv_heads, head_dim, as_stream(stream)),
+                     "rth_rope_bf16");
+}
+
+int rth_rope_append_fp8(uint16_t* q, uint8_t* k_cache, uint8_t* v_cache, float* k_scale,
+                        float* v_scale, const uint16_t* k, const uint16_t* v,
+                        const int* positions, const float* inv_freq, const int* at_pos,
+                        int n_new, int num_q_heads, int num_kv_heads, int head_dim,
+                        void* stream) {
+    RTH_REQUIRE(q != nullptr && k != nullptr && v != nullptr, "q, k and v must not be null");
+    RTH_REQUIRE(k_cache != nullptr && v_cache != nullptr && k_scale != nullptr &&
+                    v_scale != nullptr,
+                "cache slabs and scales must not be null");
+    RTH_REQUIRE(positions != nullptr && inv_freq != nullptr && at_pos != nullptr,
+                "positions, inv_freq and at_pos must not be null");
+    RTH_REQUIRE(n_new >= 1, "n_new must be >= 1");
+    RTH_REQUIRE(num_q_heads >= 1, "num_q_heads must be >= 1");
+    RTH_REQUIRE(num_kv_heads >= 1, "num_kv_heads must be >= 1");
+    RTH_REQUIRE(head_dim == 64 || head_dim == 128 || head_dim == 256,
+                "head_dim must be one of 64, 128, 256");
+    return check_hip(rth::rope_append_fp8_launch(q, k_cache, v_cache, k_scale, v_scale, k, v,
+                                                 positions, inv_freq, at_pos, n_new,
+                                                 num_q_heads, num_kv_heads, head_dim,
+                                                 as_stream(stream)),
+                     "rth_rope_append_fp8");
+}
+
 int rth_advance_position(int* pos, int delta, void* stream) {
     RTH_REQUIRE(pos != nullptr, "pos must not be null");
     return check_hip(rth::advance_position_launch(pos, delta, as_stream(stream)),

@@ -52,4 +52,15 @@ hipError_t attention_naive_launch(uint16_t* out, const uint16_t* q,
 
 hipError_t advance_position_launch(int* pos, int delta, hipStream_t stream);
 
+hipError_t rope_bf16_launch(uint16_t* q, uint16_t* k, const int* positions,
+                            const float* inv_freq, int seq_len, int num_q_heads,
+                            int num_kv_heads, int head_dim, hipStream_t stream);
+
+hipError_t rope_append_fp8_launch(uint16_t* q, uint8_t* k_cache, uint8_t* v_cache,
+                                  float* k_scale, float* v_scale, const uint16_t* k,
+                                  const uint16_t* v, const int* positions,
+                                  const float* inv_freq, const int* at_pos, int n_new,
+                                  int num_q_heads, int num_kv_heads, int head_dim,
+                                  hipStream_t stream);
+
 }  // namespace rth

@@ -117,6 +117,31 @@ def advance_position(pos, delta=1, stream=None):
     _ffi.call("rth_advance_position", _p(pos), int(delta), _stream(stream))
 
 
+def rope_bf16(q, k, positions, inv_freq, seq_len, num_q_heads, num_kv_heads, head_dim,
+              stream=None):
+    """In-place rotate-half RoPE on q and k (reference
+    include/runtherder/kernels/rope.cuh:16-25)."""
+    _need(q, torch.bfloat16, "q"); _need(k, torch.bfloat16, "k")
+    _need(positions, torch.int32, "positions"); _need(inv_freq, torch.float32, "inv_freq")
+    _ffi.call("rth_rope_bf16", _p(q), _p(k), _p(positions), _p(inv_freq), seq_len,
+              num_q_heads, num_kv_heads, head_dim, _stream(stream))
+
+
+def rope_append_fp8(q, k_cache, v_cache, k_scale, v_scale, k, v, positions, inv_freq, at_pos,
+                    n_new, num_q_heads, num_kv_heads, head_dim, stream=None):
+    """rope_bf16(q, k) + KV append in one launch; q rotated in place, k left
+    unrotated, cache bytes identical to the two-step sequence (no reference
+    counterpart; replaces reference src/model/supported/llama/llama3.cu:228-232)."""
+    _need(q, torch.bfloat16, "q"); _need(k, torch.bfloat16, "k"); _need(v, torch.bfloat16, "v")
+    _need(k_cache, torch.uint8, "k_cache"); _need(v_cache, torch.uint8, "v_cache")
+    _need(k_scale, torch.float32, "k_scale"); _need(v_scale, torch.float32, "v_scale")
+    _need(positions, torch.int32, "positions"); _need(inv_freq, torch.float32, "inv_freq")
+    _need(at_pos, torch.int32, "at_pos")
+    _ffi.call("rth_rope_append_fp8", _p(q), _p(k_cache), _p(v_cache), _p(k_scale), _p(v_scale),
+              _p(k), _p(v), _p(positions), _p(inv_freq), _p(at_pos), n_new, num_q_heads,
+              num_kv_heads, head_dim, _stream(stream))
+
+
 # ---- interface -------------------------------------------------------------
 
 @dataclass(frozen=True)
@@ -167,6 +192,17 @@ class KVCache:
         _ffi.call("rth_kv_append_fp8", _p(self.k[layer]), _p(self.v[layer]),
                   _p(self.k_scale[layer]), _p(self.v_scale[layer]), _p(k), _p(v),
                   _p(at_pos), n_new, self.num_kv_heads, self.head_dim, _stream(stream))
+
+    def append_rope(self, layer, q, k, v, n_new, positions, inv_freq, at_pos, num_q_heads,
+                    stream=None):
+        """RoPE on q (in place) and k, then append k, v, in one launch."""
+        if not 0 <= layer < self.num_layers:
+            raise ValueError("KVCache append layer out of range")
+        if n_new < 1:
+            raise ValueError("KVCache append n_new must be >= 1")
+        rope_append_fp8(q, self.k[layer], self.v[layer], self.k_scale[layer],
+                        self.v_scale[layer], k, v, positions, inv_freq, at_pos, n_new,
+                        num_q_heads, self.num_kv_heads, self.head_dim, stream)
 
     def view(self, layer) -> KVView:
         if not 0 <= layer < self.num_layers:

@@ -44,3 +44,7 @@ def host(t: torch.Tensor) -> np.ndarray:
 
 def sync() -> None:
     torch.cuda.synchronize()
+
+
+def i32_dev(a: np.ndarray) -> torch.Tensor:
+    return torch.from_numpy(np.ascontiguousarray(a, dtype=np.int32)).to(DEV)

@@ -85,6 +85,7 @@ def test_cpp_headers_compile():
 #include <runtherder/kernels/flash_decode.h>
 #include <runtherder/kernels/flash_prefill.h>
 #include <runtherder/kernels/attention.h>
+#include <runtherder/kernels/rope.h>
 static_assert(sizeof(runtherder::attention::KVView) == 4 * sizeof(void*));
 int main() { return 0; }
 """
@@ -92,3 +93,13 @@ int main() { return 0; }
                           f"-I{ROOT / 'include'}", "--offload-arch=gfx950", "-"],
                          input=src, capture_output=True, text=True)
     assert res.returncode == 0, res.stderr[-3000:]
+
+
+def test_rope_rejects_bad_shapes():
+    assert "even" in _err("rth_rope_bf16", FAKE, FAKE, FAKE, FAKE, 4, 32, 8, 127, None)
+    assert "256" in _err("rth_rope_bf16", FAKE, FAKE, FAKE, FAKE, 4, 32, 8, 258, None)
+    assert "seq_len" in _err("rth_rope_bf16", FAKE, FAKE, FAKE, FAKE, 0, 32, 8, 128, None)
+    assert "head_dim" in _err("rth_rope_append_fp8", FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE,
+                              FAKE, FAKE, FAKE, 4, 32, 8, 96, None)
+    assert "at_pos" in _err("rth_rope_append_fp8", FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE,
+                            FAKE, FAKE, None, 4, 32, 8, 128, None)
