@@ -15,6 +15,7 @@
 
 #include <runtherder/attention/factory.h>
 #include <runtherder/engine/kv_cache.h>
+#include <runtherder/kernels/rope.h>
 
 #include "rth_oracle.h"
 
@@ -136,12 +137,108 @@ int run_case(BackendKind kind, const char* name) {
     return fails;
 }
 
+// KVCache::append_rope against kernels::rope_bf16 followed by
+// KVCache::append (the reference's caller order, llama3.cu:228-232), and both
+// against the oracle's RoPE then quantize; cache bytes and the rotated q must
+// match bit for bit.
+int run_rope_case() {
+    const int Hq = 32, Hkv = 8, D = 128, n = 257, at = 40, max_seq = at + n;
+    std::vector<uint16_t> qh(static_cast<size_t>(n) * Hq * D), kh(static_cast<size_t>(n) * Hkv * D),
+        vh(kh.size());
+    rth_ref_fill_normal_bf16(qh.data(), static_cast<int64_t>(qh.size()), 900);
+    rth_ref_fill_normal_bf16(kh.data(), static_cast<int64_t>(kh.size()), 901);
+    rth_ref_fill_normal_bf16(vh.data(), static_cast<int64_t>(vh.size()), 902);
+    std::vector<int>   posh(n);
+    std::vector<float> inv(D / 2);
+    for (int t = 0; t < n; ++t) {
+        posh[t] = at + t;
+    }
+    rth_ref_rope_inv_freq_llama3(inv.data(), D, 5e5f, 32.0f, 1.0f, 4.0f, 8192);
+
+    auto* dq1 = dev_alloc<uint16_t>(qh.size());
+    auto* dq2 = dev_alloc<uint16_t>(qh.size());
+    auto* dk  = dev_alloc<uint16_t>(kh.size());
+    auto* dk2 = dev_alloc<uint16_t>(kh.size());
+    auto* dv  = dev_alloc<uint16_t>(vh.size());
+    auto* dpos = dev_alloc<int>(n);
+    auto* dinv = dev_alloc<float>(inv.size());
+    int*  dat  = dev_alloc<int>(1);
+    RUNTHERDER_HIP_CHECK(hipMemcpy(dq1, qh.data(), qh.size() * 2, hipMemcpyHostToDevice));
+    RUNTHERDER_HIP_CHECK(hipMemcpy(dq2, qh.data(), qh.size() * 2, hipMemcpyHostToDevice));
+    RUNTHERDER_HIP_CHECK(hipMemcpy(dk, kh.data(), kh.size() * 2, hipMemcpyHostToDevice));
+    RUNTHERDER_HIP_CHECK(hipMemcpy(dk2, kh.data(), kh.size() * 2, hipMemcpyHostToDevice));
+    RUNTHERDER_HIP_CHECK(hipMemcpy(dv, vh.data(), vh.size() * 2, hipMemcpyHostToDevice));
+    RUNTHERDER_HIP_CHECK(hipMemcpy(dpos, posh.data(), n * sizeof(int), hipMemcpyHostToDevice));
+    RUNTHERDER_HIP_CHECK(hipMemcpy(dinv, inv.data(), inv.size() * 4, hipMemcpyHostToDevice));
+    RUNTHERDER_HIP_CHECK(hipMemcpy(dat, &at, sizeof(int), hipMemcpyHostToDevice));
+
+    KVCache fused(1, max_seq, Hkv, D), two(1, max_seq, Hkv, D);
+    fused.append_rope(0, reinterpret_cast<__hip_bfloat16*>(dq1),
+                      reinterpret_cast<const __hip_bfloat16*>(dk),
+                      reinterpret_cast<const __hip_bfloat16*>(dv), n, dpos, dinv, dat, Hq,
+                      nullptr);
+    runtherder::kernels::rope_bf16(reinterpret_cast<__hip_bfloat16*>(dq2),
+                                   reinterpret_cast<__hip_bfloat16*>(dk2), dpos, dinv, n, Hq,
+                                   Hkv, D, nullptr);
+    two.append(0, reinterpret_cast<const __hip_bfloat16*>(dk2),
+               reinterpret_cast<const __hip_bfloat16*>(dv), n, dat, nullptr);
+    RUNTHERDER_HIP_CHECK(hipDeviceSynchronize());
+
+    const size_t rows = static_cast<size_t>(n) * Hkv;
+    const size_t off  = static_cast<size_t>(at) * Hkv;
+    auto fetch = [&](const runtherder::attention::KVView& kv, std::vector<uint8_t>& k8,
+                     std::vector<uint8_t>& v8, std::vector<float>& ks, std::vector<float>& vs) {
+        k8.resize(rows * D);
+        v8.resize(rows * D);
+        ks.resize(rows);
+        vs.resize(rows);
+        RUNTHERDER_HIP_CHECK(hipMemcpy(k8.data(), reinterpret_cast<const uint8_t*>(kv.k) + off * D,
+                                       rows * D, hipMemcpyDeviceToHost));
+        RUNTHERDER_HIP_CHECK(hipMemcpy(v8.data(), reinterpret_cast<const uint8_t*>(kv.v) + off * D,
+                                       rows * D, hipMemcpyDeviceToHost));
+        RUNTHERDER_HIP_CHECK(hipMemcpy(ks.data(), kv.k_scale + off, rows * 4, hipMemcpyDeviceToHost));
+        RUNTHERDER_HIP_CHECK(hipMemcpy(vs.data(), kv.v_scale + off, rows * 4, hipMemcpyDeviceToHost));
+    };
+    std::vector<uint8_t> k1, v1, k2, v2;
+    std::vector<float>   ks1, vs1, ks2, vs2;
+    fetch(fused.view(0), k1, v1, ks1, vs1);
+    fetch(two.view(0), k2, v2, ks2, vs2);
+    std::vector<uint16_t> q1(qh.size()), q2(qh.size());
+    RUNTHERDER_HIP_CHECK(hipMemcpy(q1.data(), dq1, qh.size() * 2, hipMemcpyDeviceToHost));
+    RUNTHERDER_HIP_CHECK(hipMemcpy(q2.data(), dq2, qh.size() * 2, hipMemcpyDeviceToHost));
+
+    std::vector<uint16_t> qr = qh, kr = kh;
+    rth_ref_rope_apply_bf16(qr.data(), posh.data(), inv.data(), n, Hq, D);
+    rth_ref_rope_apply_bf16(kr.data(), posh.data(), inv.data(), n, Hkv, D);
+    std::vector<uint8_t> wk(rows * D), wv(rows * D);
+    std::vector<float>   wks(rows), wvs(rows);
+    rth_ref_quantize_kv_fp8(wk.data(), wks.data(), kr.data(), 0, 1, static_cast<int>(rows), D);
+    rth_ref_quantize_kv_fp8(wv.data(), wvs.data(), vh.data(), 0, 1, static_cast<int>(rows), D);
+
+    const bool same_two = k1 == k2 && v1 == v2 &&
+                          std::memcmp(ks1.data(), ks2.data(), rows * 4) == 0 &&
+                          std::memcmp(vs1.data(), vs2.data(), rows * 4) == 0 && q1 == q2;
+    const bool same_ref = k1 == wk && v1 == wv &&
+                          std::memcmp(ks1.data(), wks.data(), rows * 4) == 0 &&
+                          std::memcmp(vs1.data(), wvs.data(), rows * 4) == 0 && q1 == qr;
+    std::printf("rope_append n=%d at=%d same_as_two_step=%d same_as_oracle=%d %s\n", n, at,
+                same_two ? 1 : 0, same_ref ? 1 : 0, (same_two && same_ref) ? "OK" : "FAIL");
+    std::fflush(stdout);
+    for (void* p : {static_cast<void*>(dq1), static_cast<void*>(dq2), static_cast<void*>(dk),
+                    static_cast<void*>(dk2), static_cast<void*>(dv), static_cast<void*>(dpos),
+                    static_cast<void*>(dinv), static_cast<void*>(dat)}) {
+        (void)hipFree(p);
+    }
+    return (same_two && same_ref) ? 0 : 1;
+}
+
 }  // namespace
 
 int main() {
     int fails = 0;
     fails += run_case(BackendKind::Adaptive, "adaptive");
     fails += run_case(BackendKind::Naive, "naive");
+    fails += run_rope_case();
     std::printf("%s\n", fails == 0 ? "ALL OK" : "FAILURES");
     return fails == 0 ? 0 : 1;
 }
