@@ -139,6 +139,35 @@ int rth_rope_append_fp8(uint16_t* q, uint8_t* k_cache, uint8_t* v_cache,
                         int num_q_heads, int num_kv_heads, int head_dim,
                         void* stream);
 
+/* No counterpart in the reference: fuses the Qwen3 caller sequence
+ * rmsnorm_bf16_forward(q, q_norm) [per q head], rmsnorm_bf16_forward(k,
+ * k_norm) [per kv head], rope_bf16(q, k), KVCache::append(k, v) (reference
+ * src/model/supported/llama/qwen3.cu:189-200) into one launch. q is
+ * normalized and rotated in place; the cache receives exactly the bytes of
+ * rth_rmsnorm_bf16 + rth_rope_bf16 + rth_kv_append_fp8; k is read only.
+ * q_norm, k_norm: [head_dim] bf16 gains. head_dim in {64, 128, 256}. */
+int rth_qk_norm_rope_append_fp8(uint16_t* q, uint8_t* k_cache, uint8_t* v_cache,
+                                float* k_scale, float* v_scale, const uint16_t* k,
+                                const uint16_t* v, const uint16_t* q_norm,
+                                const uint16_t* k_norm, float eps, const int* positions,
+                                const float* inv_freq, const int* at_pos, int n_new,
+                                int num_q_heads, int num_kv_heads, int head_dim,
+                                void* stream);
+
+/* Replaces kernels::rmsnorm_bf16_forward (reference include/runtherder/
+ * kernels/rmsnorm.cuh:14-22): y = bf16((x * rrms) * g) per row of
+ * x [num_tokens, hidden_dim] bf16, rrms = 1 / sqrt(sum(x^2) / hidden_dim +
+ * eps) with a correctly rounded sqrt and division; y may alias x.
+ * hidden_dim a multiple of 8, <= 16384. The sum of squares runs over
+ * rth_rmsnorm_lanes(hidden_dim) lane partials in a fixed order. */
+int rth_rmsnorm_bf16(uint16_t* y, const uint16_t* x, const uint16_t* g, int num_tokens,
+                     int hidden_dim, float eps, void* stream);
+
+/* Lanes per row of rth_rmsnorm_bf16's reduction (the next power of two of
+ * hidden_dim / 8, at most 64); 0 for an invalid hidden_dim. No reference
+ * counterpart: lets a checker restate the summation order. */
+int rth_rmsnorm_lanes(int hidden_dim);
+
 #ifdef __cplusplus
 }
 #endif

@@ -86,6 +86,30 @@ public:
             num_q_heads, num_kv_heads_, head_dim_, stream));
     }
 
+    // Qwen3 order in one launch (no reference counterpart; the caller
+    // sequence it replaces is reference src/model/supported/llama/
+    // qwen3.cu:189-200): per-head RMSNorm of q and k with gains q_norm,
+    // k_norm [head_dim], RoPE, append. q is updated in place; k is read only.
+    void append_qk_norm_rope(int layer, __hip_bfloat16* q, const __hip_bfloat16* k,
+                             const __hip_bfloat16* v, int n_new, const __hip_bfloat16* q_norm,
+                             const __hip_bfloat16* k_norm, float eps, const int* positions,
+                             const float* inv_freq, const int* at_pos, int num_q_heads,
+                             hipStream_t stream) {
+        RUNTHERDER_CHECK(layer >= 0 && layer < num_layers_, "KVCache append layer out of range");
+        RUNTHERDER_CHECK(n_new >= 1, "KVCache append n_new must be >= 1");
+        RUNTHERDER_CHECK(at_pos != nullptr, "KVCache append at_pos must not be null");
+        const std::size_t dst  = static_cast<std::size_t>(layer) * layer_stride_;
+        const std::size_t sdst = static_cast<std::size_t>(layer) * scale_layer_stride_;
+        RUNTHERDER_RTH_CHECK(rth_qk_norm_rope_append_fp8(
+            reinterpret_cast<std::uint16_t*>(q), reinterpret_cast<std::uint8_t*>(k_.get() + dst),
+            reinterpret_cast<std::uint8_t*>(v_.get() + dst), k_scale_.get() + sdst,
+            v_scale_.get() + sdst, reinterpret_cast<const std::uint16_t*>(k),
+            reinterpret_cast<const std::uint16_t*>(v),
+            reinterpret_cast<const std::uint16_t*>(q_norm),
+            reinterpret_cast<const std::uint16_t*>(k_norm), eps, positions, inv_freq, at_pos,
+            n_new, num_q_heads, num_kv_heads_, head_dim_, stream));
+    }
+
     [[nodiscard]] attention::KVView view(int layer) const {
         RUNTHERDER_CHECK(layer >= 0 && layer < num_layers_, "KVCache view layer out of range");
         const std::size_t base  = static_cast<std::size_t>(layer) * layer_stride_;

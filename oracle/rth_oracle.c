@@ -27,7 +27,13 @@
  *                             empty splits.
  *   rth_ref_rope_*            closed forms (position 0 is identity, rotation
  *                             preserves pair norms, plain table is
- *                             theta^(-2i/D)); input preparation only.
+ *                             theta^(-2i/D)); rope_apply against an
+ *                             independent numpy restatement and the
+ *                             reference's own bound (max-abs 5e-2 vs double).
+ *   rth_ref_rmsnorm_bf16      the reference test's own CPU formula (double sum
+ *                             of squares, tests/kernels/test_rmsnorm.cpp:39-60)
+ *                             within one bf16 ulp, closed forms (constant rows,
+ *                             scale invariance, unit gain).
  */
 #include "rth_oracle.h"
 
@@ -739,6 +745,46 @@ void rth_ref_rope_apply_bf16(uint16_t* x, const int* positions,
                 row[i]         = rth_ref_f32_to_bf16(fmaf(a, c, -(b * s)));
                 row[i + half]  = rth_ref_f32_to_bf16(fmaf(a, s, b * c));
             }
+        }
+    }
+}
+
+/* RMSNorm of each row of x[rows, dim] bf16 with gain g[dim] bf16
+ * (src/kernels/rmsnorm.cu:45-136, rmsnorm_bf16_forward): y = bf16((x * rrms) * g)
+ * with rrms = 1 / sqrt(ss / dim + eps) (the reference kernel uses rsqrtf; its
+ * test oracle, tests/kernels/test_rmsnorm.cpp:39-60, 1.0f / std::sqrt). The sum
+ * of squares is taken in the order of the GPU kernel: `lanes` (a power of
+ * two) partial sums, lane l accumulating fmaf(x, x, s) over the 8-element
+ * vectors l, l + lanes, ... (elements in order), then a butterfly over the
+ * lanes (s_l + s_(l^1), then ^2, ^4, ...), which every lane ends with. */
+void rth_ref_rmsnorm_bf16(uint16_t* y, const uint16_t* x, const uint16_t* g,
+                          int rows, int dim, float eps, int lanes) {
+    float part[64];
+    for (int r = 0; r < rows; ++r) {
+        const uint16_t* xr = x + (int64_t)r * dim;
+        for (int l = 0; l < lanes; ++l) {
+            float s = 0.0f;
+            for (int v = l; v < dim / 8; v += lanes) {
+                for (int j = 0; j < 8; ++j) {
+                    const float h = rth_ref_bf16_to_f32(xr[8 * v + j]);
+                    s             = fmaf(h, h, s);
+                }
+            }
+            part[l] = s;
+        }
+        for (int m = 1; m < lanes; m <<= 1) {
+            float nxt[64];
+            for (int l = 0; l < lanes; ++l) {
+                nxt[l] = part[l] + part[l ^ m];
+            }
+            memcpy(part, nxt, sizeof(float) * (size_t)lanes);
+        }
+        const float t    = part[0] / (float)dim + eps;
+        const float rrms = 1.0f / sqrtf(t);
+        uint16_t*   yr   = y + (int64_t)r * dim;
+        for (int d = 0; d < dim; ++d) {
+            const float h = rth_ref_bf16_to_f32(xr[d]);
+            yr[d]         = rth_ref_f32_to_bf16((h * rrms) * rth_ref_bf16_to_f32(g[d]));
         }
     }
 }

@@ -73,6 +73,8 @@ void rth_ref_rope_inv_freq_llama3(float* inv_freq, int head_dim,
                                   float low_freq_factor,
                                   float high_freq_factor,
                                   int original_max_position_embeddings);
+void rth_ref_rmsnorm_bf16(uint16_t* y, const uint16_t* x, const uint16_t* g,
+                          int rows, int dim, float eps, int lanes);
 void rth_ref_rope_apply_bf16(uint16_t* x, const int* positions,
                              const float* inv_freq, int n_tokens,
                              int num_heads, int head_dim);

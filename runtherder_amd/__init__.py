@@ -24,7 +24,10 @@ from .ops import (  # noqa: F401
     make_attention_backend,
     new_flash_split_scratch,
     quantize_kv_fp8,
+    qk_norm_rope_append_fp8,
     quantize_kv_fp8_scaled,
+    rmsnorm_bf16,
+    rmsnorm_lanes,
     rope_append_fp8,
     rope_bf16,
 )

@@ -31,6 +31,11 @@ _SIGNATURES = {
     "rth_rope_bf16": (_c_int, [_vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, _c_int, _vp]),
     "rth_rope_append_fp8": (_c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
                                      _c_int, _c_int, _c_int, _c_int, _vp]),
+    "rth_qk_norm_rope_append_fp8": (_c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
+                                             ctypes.c_float, _vp, _vp, _vp, _c_int, _c_int,
+                                             _c_int, _c_int, _vp]),
+    "rth_rmsnorm_bf16": (_c_int, [_vp, _vp, _vp, _c_int, _c_int, ctypes.c_float, _vp]),
+    "rth_rmsnorm_lanes": (_c_int, [_c_int]),
 }
 
 _lib: ctypes.CDLL | None = None

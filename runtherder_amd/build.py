@@ -42,6 +42,7 @@ KERNEL_SOURCES = [
     "flash_prefill.hip",
     "attention_naive.hip",
     "rope.hip",
+    "rmsnorm.hip",
     "capi.cpp",
 ]
 HOST_SOURCES = ["attention_backends.cpp"]

@@ -248,10 +248,56 @@ int rth_rope_append_fp8(uint16_t* q, uint8_t* k_cache, uint8_t* v_cache, float* 
     RTH_REQUIRE(head_dim == 64 || head_dim == 128 || head_dim == 256,
                 "head_dim must be one of 64, 128, 256");
     return check_hip(rth::rope_append_fp8_launch(q, k_cache, v_cache, k_scale, v_scale, k, v,
-                                                 positions, inv_freq, at_pos, n_new,
-                                                 num_q_heads, num_kv_heads, head_dim,
-                                                 as_stream(stream)),
+                                                 nullptr, nullptr, 0.0f, positions, inv_freq,
+                                                 at_pos, n_new, num_q_heads, num_kv_heads,
+                                                 head_dim, as_stream(stream)),
                      "rth_rope_append_fp8");
+}
+
+int rth_qk_norm_rope_append_fp8(uint16_t* q, uint8_t* k_cache, uint8_t* v_cache,
+                                float* k_scale, float* v_scale, const uint16_t* k,
+                                const uint16_t* v, const uint16_t* q_norm,
+                                const uint16_t* k_norm, float eps, const int* positions,
+                                const float* inv_freq, const int* at_pos, int n_new,
+                                int num_q_heads, int num_kv_heads, int head_dim,
+                                void* stream) {
+    RTH_REQUIRE(q != nullptr && k != nullptr && v != nullptr, "q, k and v must not be null");
+    RTH_REQUIRE(k_cache != nullptr && v_cache != nullptr && k_scale != nullptr &&
+                    v_scale != nullptr,
+                "cache slabs and scales must not be null");
+    RTH_REQUIRE(q_norm != nullptr && k_norm != nullptr, "q_norm and k_norm must not be null");
+    RTH_REQUIRE(eps > 0.0f, "eps must be > 0");
+    RTH_REQUIRE(positions != nullptr && inv_freq != nullptr && at_pos != nullptr,
+                "positions, inv_freq and at_pos must not be null");
+    RTH_REQUIRE(n_new >= 1, "n_new must be >= 1");
+    RTH_REQUIRE(num_q_heads >= 1, "num_q_heads must be >= 1");
+    RTH_REQUIRE(num_kv_heads >= 1, "num_kv_heads must be >= 1");
+    RTH_REQUIRE(head_dim == 64 || head_dim == 128 || head_dim == 256,
+                "head_dim must be one of 64, 128, 256");
+    return check_hip(rth::rope_append_fp8_launch(q, k_cache, v_cache, k_scale, v_scale, k, v,
+                                                 q_norm, k_norm, eps, positions, inv_freq,
+                                                 at_pos, n_new, num_q_heads, num_kv_heads,
+                                                 head_dim, as_stream(stream)),
+                     "rth_qk_norm_rope_append_fp8");
+}
+
+int rth_rmsnorm_bf16(uint16_t* y, const uint16_t* x, const uint16_t* g, int num_tokens,
+                     int hidden_dim, float eps, void* stream) {
+    // Checks of rmsnorm_bf16_forward (reference src/kernels/rmsnorm.cu:172-176).
+    RTH_REQUIRE(y != nullptr && x != nullptr && g != nullptr, "y, x and g must not be null");
+    RTH_REQUIRE(num_tokens >= 1, "num_tokens must be >= 1");
+    RTH_REQUIRE(hidden_dim >= 8, "hidden_dim must be >= 8");
+    RTH_REQUIRE(hidden_dim % 8 == 0,
+                "hidden_dim must be divisible by 8 for BF16 vectorized load");
+    RTH_REQUIRE(hidden_dim <= 16384, "hidden_dim too large for current dispatch");
+    RTH_REQUIRE(eps > 0.0f, "eps must be > 0");
+    return check_hip(rth::rmsnorm_bf16_launch(y, x, g, num_tokens, hidden_dim, eps,
+                                              as_stream(stream)),
+                     "rth_rmsnorm_bf16");
+}
+
+int rth_rmsnorm_lanes(int hidden_dim) {
+    return (hidden_dim >= 8 && hidden_dim % 8 == 0) ? rth::rmsnorm_lanes(hidden_dim) : 0;
 }
 
 int rth_advance_position(int* pos, int delta, void* stream) {

@@ -56,11 +56,19 @@ hipError_t rope_bf16_launch(uint16_t* q, uint16_t* k, const int* positions,
                             const float* inv_freq, int seq_len, int num_q_heads,
                             int num_kv_heads, int head_dim, hipStream_t stream);
 
+// q_norm == nullptr: RoPE + append; otherwise per-head RMSNorm of q and k
+// (gains q_norm, k_norm [head_dim]) before the RoPE.
 hipError_t rope_append_fp8_launch(uint16_t* q, uint8_t* k_cache, uint8_t* v_cache,
                                   float* k_scale, float* v_scale, const uint16_t* k,
-                                  const uint16_t* v, const int* positions,
+                                  const uint16_t* v, const uint16_t* q_norm,
+                                  const uint16_t* k_norm, float eps, const int* positions,
                                   const float* inv_freq, const int* at_pos, int n_new,
                                   int num_q_heads, int num_kv_heads, int head_dim,
                                   hipStream_t stream);
+
+int rmsnorm_lanes(int dim);
+
+hipError_t rmsnorm_bf16_launch(uint16_t* y, const uint16_t* x, const uint16_t* g, int rows,
+                               int dim, float eps, hipStream_t stream);
 
 }  // namespace rth

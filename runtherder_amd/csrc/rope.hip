@@ -24,6 +24,7 @@
 // those of rope_bf16 followed by the append, bit for bit.
 #include "device_common.hpp"
 #include "launch.hpp"
+#include "rmsnorm_row.hpp"
 
 namespace rth {
 namespace {
@@ -145,46 +146,64 @@ __device__ __forceinline__ void quantize_row_regs(const u32x4 w4, int sub, uint8
     *reinterpret_cast<u32x2*>(qrow + 8 * sub) = out;
 }
 
-// kLpr = head_dim / 8 lanes per cache row; the RoPE partner of lane l's
-// elements sits in lane l ^ (kLpr / 2).
+// Rotates one row held as one vector per lane (kLpr lanes, head_dim =
+// 8 * kLpr): the RoPE partner of lane l's elements sits in lane l ^ (kLpr/2).
 template <int kLpr>
+__device__ __forceinline__ u32x4 rope_vec(const u32x4 w4, int sub, const float* sm_c,
+                                          const float* sm_s) {
+    u32x4 other;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        other[e] = static_cast<uint32_t>(__shfl_xor(static_cast<int>(w4[e]), kLpr / 2, kWave));
+    }
+    const bool first = sub < kLpr / 2;
+    u32x4      a     = first ? w4 : other;
+    u32x4      b     = first ? other : w4;
+    rotate8(a, b, sm_c, sm_s, 8 * (first ? sub : sub - kLpr / 2));
+    return first ? a : b;
+}
+
+// Per token: q rows [optional RMSNorm] -> RoPE -> stored in place; K rows
+// [optional RMSNorm] -> RoPE -> quantized into the cache; V rows quantized.
+// A row is one group of kLpr lanes; every lane of a group takes the same
+// branch and trip count, so the shuffles stay within converged groups.
+template <int kLpr, bool kNorm>
 __global__ __launch_bounds__(kRopeBlock) void rope_append_kernel(
     uint16_t* __restrict__ q, uint8_t* __restrict__ k_cache, uint8_t* __restrict__ v_cache,
     float* __restrict__ k_scale, float* __restrict__ v_scale, const uint16_t* __restrict__ k,
-    const uint16_t* __restrict__ v, const int* __restrict__ positions,
+    const uint16_t* __restrict__ v, const uint16_t* __restrict__ q_norm,
+    const uint16_t* __restrict__ k_norm, float eps, const int* __restrict__ positions,
     const float* __restrict__ inv_freq, const int* __restrict__ at_pos, int hq, int hkv) {
     constexpr int kHeadDim = 8 * kLpr;
-    constexpr int kHalf    = kHeadDim / 2;
     constexpr int kRowsPB  = kRopeBlock / kLpr;
     __shared__ __attribute__((aligned(16))) float sm_c[kRopeMaxHalf];
     __shared__ __attribute__((aligned(16))) float sm_s[kRopeMaxHalf];
 
     const int t = static_cast<int>(blockIdx.x);
-    rope_table(sm_c, sm_s, positions[t], inv_freq, kHalf);
+    rope_table(sm_c, sm_s, positions[t], inv_freq, kHeadDim / 2);
     __syncthreads();
-    rope_rows<true>(q + static_cast<int64_t>(t) * hq * kHeadDim, hq, kHeadDim, sm_c, sm_s);
 
     const int     sub  = static_cast<int>(threadIdx.x) % kLpr;
     const int64_t row0 = static_cast<int64_t>(*at_pos + t) * hkv;
-    // Rows 0 .. hkv-1 are K (rotated), hkv .. 2hkv-1 are V. Every lane of a
-    // row group takes the same trip count, so the shuffles stay converged.
-    for (int r = static_cast<int>(threadIdx.x) / kLpr; r < 2 * hkv; r += kRowsPB) {
-        const bool      is_k = r < hkv;
-        const int       h    = is_k ? r : r - hkv;
+    for (int r = static_cast<int>(threadIdx.x) / kLpr; r < hq + 2 * hkv; r += kRowsPB) {
+        if (r < hq) {
+            uint16_t* xr = q + (static_cast<int64_t>(t) * hq + r) * kHeadDim + 8 * sub;
+            u32x4     w4 = *reinterpret_cast<const u32x4*>(xr);
+            if constexpr (kNorm) {
+                w4 = rmsnorm_vec<kLpr>(w4, q_norm, sub, eps);
+            }
+            *reinterpret_cast<u32x4*>(xr) = rope_vec<kLpr>(w4, sub, sm_c, sm_s);
+            continue;
+        }
+        const bool      is_k = r < hq + hkv;
+        const int       h    = is_k ? r - hq : r - hq - hkv;
         const uint16_t* xr   = (is_k ? k : v) + (static_cast<int64_t>(t) * hkv + h) * kHeadDim;
         u32x4           w4   = *reinterpret_cast<const u32x4*>(xr + 8 * sub);
         if (is_k) {
-            u32x4 other;
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                other[e] = static_cast<uint32_t>(
-                    __shfl_xor(static_cast<int>(w4[e]), kLpr / 2, kWave));
+            if constexpr (kNorm) {
+                w4 = rmsnorm_vec<kLpr>(w4, k_norm, sub, eps);
             }
-            const bool first = sub < kLpr / 2;
-            u32x4      a     = first ? w4 : other;
-            u32x4      b     = first ? other : w4;
-            rotate8(a, b, sm_c, sm_s, 8 * (first ? sub : sub - kLpr / 2));
-            w4 = first ? a : b;
+            w4 = rope_vec<kLpr>(w4, sub, sm_c, sm_s);
         }
         const int64_t dst = row0 + h;
         quantize_row_regs<kLpr>(w4, sub, (is_k ? k_cache : v_cache) + dst * kHeadDim,
@@ -210,17 +229,27 @@ hipError_t rope_bf16_launch(uint16_t* q, uint16_t* k, const int* positions,
 
 hipError_t rope_append_fp8_launch(uint16_t* q, uint8_t* k_cache, uint8_t* v_cache,
                                   float* k_scale, float* v_scale, const uint16_t* k,
-                                  const uint16_t* v, const int* positions,
+                                  const uint16_t* v, const uint16_t* q_norm,
+                                  const uint16_t* k_norm, float eps, const int* positions,
                                   const float* inv_freq, const int* at_pos, int n_new,
                                   int num_q_heads, int num_kv_heads, int head_dim,
                                   hipStream_t stream) {
     const dim3 grid(static_cast<unsigned>(n_new));
+    const bool norm = q_norm != nullptr;
     switch (head_dim) {
-#define RTH_RA_CASE(D)                                                                  \
-    case D:                                                                             \
-        hipLaunchKernelGGL(rope_append_kernel<D / 8>, grid, dim3(kRopeBlock), 0, stream, \
-                           q, k_cache, v_cache, k_scale, v_scale, k, v, positions,       \
-                           inv_freq, at_pos, num_q_heads, num_kv_heads);                 \
+#define RTH_RA_CASE(D)                                                                      \
+    case D:                                                                                 \
+        if (norm) {                                                                         \
+            hipLaunchKernelGGL((rope_append_kernel<D / 8, true>), grid, dim3(kRopeBlock), 0, \
+                               stream, q, k_cache, v_cache, k_scale, v_scale, k, v, q_norm, \
+                               k_norm, eps, positions, inv_freq, at_pos, num_q_heads,       \
+                               num_kv_heads);                                              \
+        } else {                                                                            \
+            hipLaunchKernelGGL((rope_append_kernel<D / 8, false>), grid, dim3(kRopeBlock), 0, \
+                               stream, q, k_cache, v_cache, k_scale, v_scale, k, v, q_norm, \
+                               k_norm, eps, positions, inv_freq, at_pos, num_q_heads,       \
+                               num_kv_heads);                                              \
+        }                                                                                   \
         break;
         RTH_RA_CASE(64)
         RTH_RA_CASE(128)

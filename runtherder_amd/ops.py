@@ -142,6 +142,37 @@ def rope_append_fp8(q, k_cache, v_cache, k_scale, v_scale, k, v, positions, inv_
               num_kv_heads, head_dim, _stream(stream))
 
 
+def qk_norm_rope_append_fp8(q, k_cache, v_cache, k_scale, v_scale, k, v, q_norm, k_norm, eps,
+                            positions, inv_freq, at_pos, n_new, num_q_heads, num_kv_heads,
+                            head_dim, stream=None):
+    """Per-head RMSNorm of q and k, RoPE, then the KV append, in one launch (no
+    reference counterpart; replaces reference
+    src/model/supported/llama/qwen3.cu:189-200). q updated in place; k read only."""
+    _need(q, torch.bfloat16, "q"); _need(k, torch.bfloat16, "k"); _need(v, torch.bfloat16, "v")
+    _need(k_cache, torch.uint8, "k_cache"); _need(v_cache, torch.uint8, "v_cache")
+    _need(k_scale, torch.float32, "k_scale"); _need(v_scale, torch.float32, "v_scale")
+    _need(q_norm, torch.bfloat16, "q_norm"); _need(k_norm, torch.bfloat16, "k_norm")
+    _need(positions, torch.int32, "positions"); _need(inv_freq, torch.float32, "inv_freq")
+    _need(at_pos, torch.int32, "at_pos")
+    _ffi.call("rth_qk_norm_rope_append_fp8", _p(q), _p(k_cache), _p(v_cache), _p(k_scale),
+              _p(v_scale), _p(k), _p(v), _p(q_norm), _p(k_norm), float(eps), _p(positions),
+              _p(inv_freq), _p(at_pos), n_new, num_q_heads, num_kv_heads, head_dim,
+              _stream(stream))
+
+
+def rmsnorm_bf16(y, x, g, num_tokens, hidden_dim, eps, stream=None):
+    """y = bf16((x * rrms) * g) per row (reference
+    include/runtherder/kernels/rmsnorm.cuh:14-22); y may alias x."""
+    _need(y, torch.bfloat16, "y"); _need(x, torch.bfloat16, "x"); _need(g, torch.bfloat16, "g")
+    _ffi.call("rth_rmsnorm_bf16", _p(y), _p(x), _p(g), num_tokens, hidden_dim, float(eps),
+              _stream(stream))
+
+
+def rmsnorm_lanes(hidden_dim: int) -> int:
+    """Lane partials of rmsnorm_bf16's sum of squares (its summation order)."""
+    return int(_ffi.load().rth_rmsnorm_lanes(hidden_dim))
+
+
 # ---- interface -------------------------------------------------------------
 
 @dataclass(frozen=True)
@@ -203,6 +234,18 @@ class KVCache:
         rope_append_fp8(q, self.k[layer], self.v[layer], self.k_scale[layer],
                         self.v_scale[layer], k, v, positions, inv_freq, at_pos, n_new,
                         num_q_heads, self.num_kv_heads, self.head_dim, stream)
+
+    def append_qk_norm_rope(self, layer, q, k, v, n_new, q_norm, k_norm, eps, positions,
+                            inv_freq, at_pos, num_q_heads, stream=None):
+        """Qwen3 order: RMSNorm of q and k per head, RoPE, then the append."""
+        if not 0 <= layer < self.num_layers:
+            raise ValueError("KVCache append layer out of range")
+        if n_new < 1:
+            raise ValueError("KVCache append n_new must be >= 1")
+        qk_norm_rope_append_fp8(q, self.k[layer], self.v[layer], self.k_scale[layer],
+                                self.v_scale[layer], k, v, q_norm, k_norm, eps, positions,
+                                inv_freq, at_pos, n_new, num_q_heads, self.num_kv_heads,
+                                self.head_dim, stream)
 
     def view(self, layer) -> KVView:
         if not 0 <= layer < self.num_layers:

@@ -36,6 +36,7 @@ _SIGS = {
     "rth_ref_rope_inv_freq_plain": (None, [_vp, _i, _f]),
     "rth_ref_rope_inv_freq_llama3": (None, [_vp, _i, _f, _f, _f, _f, _i]),
     "rth_ref_rope_apply_bf16": (None, [_vp, _vp, _vp, _i, _i, _i]),
+    "rth_ref_rmsnorm_bf16": (None, [_vp, _vp, _vp, _i, _i, _f, _i]),
 }
 
 _lib = None
@@ -204,6 +205,17 @@ def rope_apply_bf16(x: np.ndarray, positions: np.ndarray, inv_freq: np.ndarray) 
     inv = np.ascontiguousarray(inv_freq, dtype=np.float32)
     lib().rth_ref_rope_apply_bf16(_ptr(x), _ptr(pos), _ptr(inv), n, h, d)
     return x
+
+
+def rmsnorm_bf16(x: np.ndarray, g: np.ndarray, eps: float, lanes: int) -> np.ndarray:
+    """Rows of x (last axis = dim) normalized with gain g, in the GPU's
+    summation order over `lanes` lane partials."""
+    x = np.ascontiguousarray(x, dtype=np.uint16)
+    g = np.ascontiguousarray(g, dtype=np.uint16)
+    dim = x.shape[-1]
+    y = np.empty_like(x)
+    lib().rth_ref_rmsnorm_bf16(_ptr(y), _ptr(x), _ptr(g), x.size // dim, dim, eps, lanes)
+    return y
 
 
 # ---- comparisons -----------------------------------------------------------

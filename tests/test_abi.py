@@ -86,6 +86,7 @@ def test_cpp_headers_compile():
 #include <runtherder/kernels/flash_prefill.h>
 #include <runtherder/kernels/attention.h>
 #include <runtherder/kernels/rope.h>
+#include <runtherder/kernels/rmsnorm.h>
 static_assert(sizeof(runtherder::attention::KVView) == 4 * sizeof(void*));
 int main() { return 0; }
 """
@@ -103,3 +104,13 @@ def test_rope_rejects_bad_shapes():
                               FAKE, FAKE, FAKE, 4, 32, 8, 96, None)
     assert "at_pos" in _err("rth_rope_append_fp8", FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE,
                             FAKE, FAKE, None, 4, 32, 8, 128, None)
+
+
+def test_rmsnorm_rejects_and_lanes():
+    assert "divisible by 8" in _err("rth_rmsnorm_bf16", FAKE, FAKE, FAKE, 4, 12,
+                                    ctypes.c_float(1e-6), None)
+    assert "eps" in _err("rth_rmsnorm_bf16", FAKE, FAKE, FAKE, 4, 128, ctypes.c_float(0.0), None)
+    assert "q_norm" in _err("rth_qk_norm_rope_append_fp8", FAKE, FAKE, FAKE, FAKE, FAKE, FAKE,
+                            FAKE, None, FAKE, ctypes.c_float(1e-6), FAKE, FAKE, FAKE, 4, 32, 8,
+                            128, None)
+    assert [R.rmsnorm_lanes(d) for d in (8, 64, 128, 256, 4096, 12)] == [1, 8, 16, 32, 64, 0]
