@@ -187,10 +187,11 @@ def bench_prefill(torch, R, stream, n=4096, iters=10):
 
 
 def bench_rope_append(torch, R, stream, n=4096, iters=20):
-    """Config-4 shapes (32Q/8KV, head_dim 128): RoPE on q and k then the K/V
-    append as two launches (rope_bf16 + append, the reference's sequence)
-    against the fused entry; algorithmic bytes of the fused call: q read and
-    written, k and v read, E4M3 codes and scales written."""
+    """Config-4 shapes (32Q/8KV, head_dim 128). Llama order: RoPE on q and k
+    then the K/V append as two launches (rope_bf16 + append) against the fused
+    entry. Qwen3 order: per-head RMSNorm of q and of k, RoPE, append (four
+    launches) against the fused entry. Algorithmic bytes of a fused call: q
+    read and written, k and v read, E4M3 codes and scales written."""
     hq, hkv, d = 32, 8, 128
     dev = torch.device("cuda:0")
     gen = torch.Generator(device=dev)
@@ -199,28 +200,46 @@ def bench_rope_append(torch, R, stream, n=4096, iters=20):
     pos = torch.zeros(1, dtype=torch.int32, device=dev)
     positions = torch.arange(n, dtype=torch.int32, device=dev)
     inv = (1e6 ** (-torch.arange(0, d, 2, dtype=torch.float64, device=dev) / d)).float()
+    eps = 1e-6
     with torch.cuda.stream(stream):
         q = torch.randn((n, hq, d), generator=gen, device=dev).to(torch.bfloat16)
         k = torch.randn((n, hkv, d), generator=gen, device=dev).to(torch.bfloat16)
         v = torch.randn((n, hkv, d), generator=gen, device=dev).to(torch.bfloat16)
-        for _ in range(2):
+        qn = torch.randn((d,), generator=gen, device=dev).to(torch.bfloat16)
+        kn = torch.randn((d,), generator=gen, device=dev).to(torch.bfloat16)
+
+        def llama_two_step():
             R.rope_bf16(q, k, positions, inv, n, hq, hkv, d)
             cache.append(0, k, v, n, pos)
+
+        def llama_fused():
             cache.append_rope(0, q, k, v, n, positions, inv, pos, hq)
-        torch.cuda.synchronize()
-        with EventTimer(torch, stream) as t2:
-            for _ in range(iters):
-                R.rope_bf16(q, k, positions, inv, n, hq, hkv, d)
-                cache.append(0, k, v, n, pos)
-        with EventTimer(torch, stream) as t1:
-            for _ in range(iters):
-                cache.append_rope(0, q, k, v, n, positions, inv, pos, hq)
+
+        def qwen_unfused():
+            R.rmsnorm_bf16(q, q, qn, n * hq, d, eps)
+            R.rmsnorm_bf16(k, k, kn, n * hkv, d, eps)
+            R.rope_bf16(q, k, positions, inv, n, hq, hkv, d)
+            cache.append(0, k, v, n, pos)
+
+        def qwen_fused():
+            cache.append_qk_norm_rope(0, q, k, v, n, qn, kn, eps, positions, inv, pos, hq)
+
+        res = {}
+        for name, fn in (("two_step_us", llama_two_step), ("fused_us", llama_fused),
+                         ("qwen_unfused_us", qwen_unfused), ("qwen_fused_us", qwen_fused)):
+            for _ in range(2):
+                fn()
+            torch.cuda.synchronize()
+            with EventTimer(torch, stream) as t:
+                for _ in range(iters):
+                    fn()
+            res[name] = round(t.ms * 1e3 / iters, 2)
     torch.cuda.synchronize()
     fused_bytes = n * hq * d * 4 + n * hkv * d * 4 + n * hkv * d * 2 + n * hkv * 8
-    us1, us2 = t1.ms * 1e3 / iters, t2.ms * 1e3 / iters
-    return {"n": n, "fused_us": round(us1, 2), "two_step_us": round(us2, 2),
-            "fused_gbs": round(fused_bytes / (us1 * 1e-6) / 1e9, 1),
-            "fused_bytes": fused_bytes}
+    res.update({"n": n, "fused_bytes": fused_bytes,
+                "fused_gbs": round(fused_bytes / (res["fused_us"] * 1e-6) / 1e9, 1),
+                "qwen_fused_gbs": round(fused_bytes / (res["qwen_fused_us"] * 1e-6) / 1e9, 1)})
+    return res
 
 
 def decode_kernel_sweep(torch, R, stream, points):
@@ -450,8 +469,9 @@ def main() -> int:
                          "flops_per_launch": pf["flops"]},
             "append_us": round(pf["append_us"], 2), "append_gbs": round(pf["append_gbs"], 1),
         },
-        "rope_append": dict(ra, workload="config4 shapes: RoPE(q,k) + K/V FP8 append, fused "
-                                         "entry vs rope_bf16 then append"),
+        "rope_append": dict(ra, workload="config4 shapes: RoPE(q,k) + K/V FP8 append (and the "
+                                         "Qwen3 q/k RMSNorm before it), fused entries vs the "
+                                         "unfused launch sequences"),
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
