@@ -90,6 +90,21 @@ int rth_attn_decode_split(uint16_t* out, const uint16_t* q, const uint8_t* k,
                           int num_kv_heads, int head_dim, float scale,
                           void* stream);
 
+/* No counterpart in the reference: KVCache::append(layer, k_new, v_new, 1,
+ * cache_len) followed by the decode call (reference
+ * src/model/supported/llama/llama3.cu:232-234 with n_new == 1) in one call
+ * of two kernels instead of three. The new token ([Hkv, D] bf16) is
+ * quantized into row *cache_len of the layer's cache slabs (bytes identical
+ * to rth_kv_append_fp8) and attended with the *cache_len earlier keys;
+ * output equals rth_kv_append_fp8 + rth_attn_decode_split. Same shapes and
+ * scratch as rth_attn_decode_split. */
+int rth_attn_decode_append_split(uint16_t* out, const uint16_t* q, uint8_t* k_cache,
+                                 uint8_t* v_cache, float* k_scale, float* v_scale,
+                                 const uint16_t* k_new, const uint16_t* v_new,
+                                 float* partial, int num_splits, const int* cache_len,
+                                 int num_q_heads, int num_kv_heads, int head_dim,
+                                 float scale, void* stream);
+
 /* Replaces kernels::flash_prefill_bf16 (reference
  * include/runtherder/kernels/flash_prefill.cuh:26-39): causal attention of
  * n_new queries at positions *cache_len .. *cache_len + n_new - 1 over keys

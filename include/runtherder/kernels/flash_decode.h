@@ -45,4 +45,31 @@ inline void flash_decode_split_bf16(__hip_bfloat16*       out,
         scale, stream));
 }
 
+// KVCache::append of one token at row *cache_len followed by
+// flash_decode_split_bf16 over *cache_len + 1 keys, as one call (no reference
+// counterpart). k, v, k_scale, v_scale are the layer's writable cache slabs;
+// k_new, v_new are [num_kv_heads, head_dim] bf16.
+inline void flash_decode_append_split_bf16(__hip_bfloat16*       out,
+                                           const __hip_bfloat16* q,
+                                           __hip_fp8_e4m3*       k,
+                                           __hip_fp8_e4m3*       v,
+                                           float*                k_scale,
+                                           float*                v_scale,
+                                           const __hip_bfloat16* k_new,
+                                           const __hip_bfloat16* v_new,
+                                           float*                partial,
+                                           int                   num_splits,
+                                           const int*            cache_len,
+                                           int                   num_q_heads,
+                                           int                   num_kv_heads,
+                                           int                   head_dim,
+                                           float                 scale,
+                                           hipStream_t           stream = nullptr) {
+    RUNTHERDER_RTH_CHECK(rth_attn_decode_append_split(
+        reinterpret_cast<std::uint16_t*>(out), reinterpret_cast<const std::uint16_t*>(q),
+        reinterpret_cast<std::uint8_t*>(k), reinterpret_cast<std::uint8_t*>(v), k_scale, v_scale,
+        reinterpret_cast<const std::uint16_t*>(k_new), reinterpret_cast<const std::uint16_t*>(v_new),
+        partial, num_splits, cache_len, num_q_heads, num_kv_heads, head_dim, scale, stream));
+}
+
 }  // namespace runtherder::kernels

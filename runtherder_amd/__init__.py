@@ -18,6 +18,7 @@ from .ops import (  # noqa: F401
     advance_position,
     attention_causal_bf16,
     default_num_splits,
+    flash_decode_append_split_bf16,
     flash_decode_split_bf16,
     flash_prefill_bf16,
     flash_split_scratch_floats,

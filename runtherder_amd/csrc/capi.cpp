@@ -175,6 +175,45 @@ int rth_attn_decode_split(uint16_t* out, const uint16_t* q, const uint8_t* k,
                      "rth_attn_decode_split");
 }
 
+int rth_attn_decode_append_split(uint16_t* out, const uint16_t* q, uint8_t* k_cache,
+                                 uint8_t* v_cache, float* k_scale, float* v_scale,
+                                 const uint16_t* k_new, const uint16_t* v_new,
+                                 float* partial, int num_splits, const int* cache_len,
+                                 int num_q_heads, int num_kv_heads, int head_dim,
+                                 float scale, void* stream) {
+    if (int rc = check_attn(out, q, k_cache, v_cache, k_scale, v_scale, cache_len)) {
+        return rc;
+    }
+    RTH_REQUIRE(k_new != nullptr && v_new != nullptr, "k_new and v_new must not be null");
+    RTH_REQUIRE(num_splits >= 1, "num_splits must be >= 1");
+    if (int rc = check_heads(num_q_heads, num_kv_heads)) {
+        return rc;
+    }
+    RTH_REQUIRE(head_dim == 32 || head_dim == 64 || head_dim == 128 || head_dim == 256 ||
+                    head_dim == 512,
+                "head_dim must be one of 32, 64, 128, 256, 512");
+    if (rth::decode_mfma_supported(num_q_heads, num_kv_heads, head_dim)) {
+        RTH_REQUIRE(partial != nullptr, "partial must not be null");
+        return check_hip(rth::flash_decode_launch(out, q, k_cache, v_cache, k_scale, v_scale,
+                                                  partial, num_splits, cache_len, num_q_heads,
+                                                  num_kv_heads, head_dim, scale,
+                                                  as_stream(stream), k_new, v_new, k_cache,
+                                                  v_cache, k_scale, v_scale),
+                         "rth_attn_decode_append_split");
+    }
+    // Shapes without the MFMA decode: the append, then the naive kernel.
+    if (int rc = check_hip(rth::kv_append_fp8_launch(k_cache, v_cache, k_scale, v_scale, k_new,
+                                                     v_new, cache_len, num_kv_heads,
+                                                     num_kv_heads, head_dim, as_stream(stream)),
+                           "rth_attn_decode_append_split")) {
+        return rc;
+    }
+    return check_hip(rth::attention_naive_launch(out, q, k_cache, v_cache, k_scale, v_scale, 1,
+                                                 cache_len, num_q_heads, num_kv_heads,
+                                                 head_dim, scale, as_stream(stream)),
+                     "rth_attn_decode_append_split");
+}
+
 int rth_attn_prefill(uint16_t* out, const uint16_t* q, const uint8_t* k,
                      const uint8_t* v, const float* k_scale,
                      const float* v_scale, int n_new, const int* cache_len,

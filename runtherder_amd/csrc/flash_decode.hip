@@ -154,12 +154,115 @@ __host__ __device__ constexpr int dec_workgroups(int num_splits, int hkv) {
                                            : (num_splits * hkv + kDecWaves - 1) / kDecWaves;
 }
 
+// The appended token's quantized K/V codes for one (kv head) unit, laid out
+// as the tile registers of key 0 of a tile (see load_tile) plus the scales.
 template <int D>
+__device__ __forceinline__ void quantize_new_token(TileRaw<D>& vt, const uint16_t* __restrict__ kx,
+                                                   const uint16_t* __restrict__ vx,
+                                                   uint8_t* kc_row, uint8_t* vc_row,
+                                                   float* ks_slot, float* vs_slot, int lane) {
+    using T     = DecTraits<D>;
+    const int n = lane & 15;
+    const int g = lane >> 4;
+    // K: lane (n = 0, g) owns bytes 16g + 64c .. +15 of the row (kraw[0][c]).
+    u32x4 kw[T::kKChunks][2];
+    float kmax = 0.0f;
+#pragma unroll
+    for (int c = 0; c < T::kKChunks; ++c) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            kw[c][h] = (n == 0) ? *reinterpret_cast<const u32x4*>(kx + 16 * g + 64 * c + 8 * h)
+                                : u32x4{0u, 0u, 0u, 0u};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                kmax = fmaxf(kmax, fabsf(__uint_as_float(kw[c][h][e] << 16)));
+                kmax = fmaxf(kmax, fabsf(__uint_as_float(kw[c][h][e] & 0xffff0000u)));
+            }
+        }
+    }
+    // V: lane (n, g = 0) owns bytes kVBytes * n .. + kVBytes - 1 (vraw[0][*]).
+    constexpr int kVW = T::kVBytes / 2;   // bf16 words
+    uint32_t      vw[kVW];
+    float         vmax = 0.0f;
+#pragma unroll
+    for (int i = 0; i < kVW; ++i) {
+        vw[i] = (g == 0) ? *reinterpret_cast<const uint32_t*>(vx + T::kVBytes * n + 2 * i) : 0u;
+        vmax  = fmaxf(vmax, fabsf(__uint_as_float(vw[i] << 16)));
+        vmax  = fmaxf(vmax, fabsf(__uint_as_float(vw[i] & 0xffff0000u)));
+    }
+    // Lanes without data hold 0, so a full-wave max leaves every lane with
+    // the row maxima (lane 32 passes the V scale to the tile registers).
+#pragma unroll
+    for (int m = 1; m < kWave; m <<= 1) {
+        kmax = wave_xor_max(kmax, m);
+        vmax = wave_xor_max(vmax, m);
+    }
+    // The append's arithmetic (quantize_rows_kernel): two separate divisions.
+    const float ksc  = kmax / kE4M3Max;
+    const float kinv = (kmax > 0.0f) ? (kE4M3Max / kmax) : 0.0f;
+    const float vsc  = vmax / kE4M3Max;
+    const float vinv = (vmax > 0.0f) ? (kE4M3Max / vmax) : 0.0f;
+    auto code4 = [](uint32_t w0, uint32_t w1, float inv) {
+        uint32_t r = 0;
+        r = e4m3x2_pack<false>(__uint_as_float(w0 << 16) * inv,
+                               __uint_as_float(w0 & 0xffff0000u) * inv, r);
+        r = e4m3x2_pack<true>(__uint_as_float(w1 << 16) * inv,
+                              __uint_as_float(w1 & 0xffff0000u) * inv, r);
+        return r;
+    };
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+#pragma unroll
+        for (int c = 0; c < T::kKChunks; ++c) {
+            vt.kraw[u][c] = u32x4{0u, 0u, 0u, 0u};
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+#pragma unroll
+        for (int w = 0; w < T::kVWords; ++w) {
+            vt.vraw[j][w] = 0u;
+        }
+    }
+#pragma unroll
+    for (int c = 0; c < T::kKChunks; ++c) {
+        u32x4 cw;
+        cw.x = code4(kw[c][0].x, kw[c][0].y, kinv);
+        cw.y = code4(kw[c][0].z, kw[c][0].w, kinv);
+        cw.z = code4(kw[c][1].x, kw[c][1].y, kinv);
+        cw.w = code4(kw[c][1].z, kw[c][1].w, kinv);
+        if (n == 0) {
+            vt.kraw[0][c] = cw;
+            *reinterpret_cast<u32x4*>(kc_row + 16 * g + 64 * c) = cw;
+        }
+    }
+#pragma unroll
+    for (int w = 0; w < T::kVWords; ++w) {
+        const uint32_t cw = code4(vw[2 * w], vw[2 * w + 1], vinv);
+        if (g == 0) {
+            vt.vraw[0][w] = cw;
+            *reinterpret_cast<uint32_t*>(vc_row + T::kVBytes * n + 4 * w) = cw;
+        }
+    }
+    vt.sc = (lane == 0) ? ksc : ((lane == 32) ? vsc : 0.0f);
+    if (lane == 0) {
+        *ks_slot = ksc;
+        *vs_slot = vsc;
+    }
+}
+
+// kAppend: the call also appends one token (k_new, v_new [Hkv, D] bf16) at
+// row *cache_len of the cache; the unit whose split holds that key quantizes
+// it, stores codes and scales, and attends to it from registers, so no wave
+// reads the row being written.
+template <int D, bool kAppend>
 __global__ __launch_bounds__(kDecThreads) void flash_decode_kernel(
     const uint16_t* __restrict__ q, const uint8_t* __restrict__ k,
     const uint8_t* __restrict__ v, const float* __restrict__ ks,
     const float* __restrict__ vs, float* __restrict__ partial, int num_splits,
-    const int* __restrict__ cache_len, int hq, int hkv, float scale_log2) {
+    const int* __restrict__ cache_len, int hq, int hkv, float scale_log2,
+    const uint16_t* __restrict__ k_new, const uint16_t* __restrict__ v_new,
+    uint8_t* k_w, uint8_t* v_w, float* ks_w, float* vs_w) {
     using T = DecTraits<D>;
 
     __shared__ __attribute__((aligned(16))) float sm_sc[kDecWaves][64];
@@ -199,11 +302,17 @@ __global__ __launch_bounds__(kDecThreads) void flash_decode_kernel(
     if (si >= pt.n_eff) {   // uniform per workgroup in coop mode
         return;
     }
-    const int k0      = si * pt.per;
-    const int k1      = min(k0 + pt.per, n_keys);
-    const int n_tiles = (k1 - k0 + kTileKeys - 1) / kTileKeys;
-    const int t_first = pt.coop ? wave : 0;
-    const int t_step  = pt.coop ? kDecWaves : 1;
+    const int k0 = si * pt.per;
+    // With an append, the split holding the new key (the last one) reads
+    // only the keys before it from the cache; one of its waves adds the new
+    // key from registers.
+    const int  p_new   = n_keys - 1;
+    const bool owner   = kAppend && (si == pt.n_eff - 1);
+    const bool virt    = owner && (!pt.coop || wave == kDecWaves - 1);
+    const int  k1      = owner ? p_new : min(k0 + pt.per, n_keys);
+    const int  n_tiles = (k1 - k0 + kTileKeys - 1) / kTileKeys;
+    const int  t_first = pt.coop ? wave : 0;
+    const int  t_step  = pt.coop ? kDecWaves : 1;
 
     // Q^T as the B operand: column n = q head of the group (zero past G).
     bf16x8 qop[T::kKSteps];
@@ -237,7 +346,7 @@ __global__ __launch_bounds__(kDecThreads) void flash_decode_kernel(
     // needs no cross-lane step and no accumulator rescale. Exact: every p and
     // l use the same reference, and p <= 2^kLazy keeps them in range.
     constexpr float kLazy = 8.0f;
-    auto process = [&](const TileRaw<D>& cur, const int kb) {
+    auto process = [&](const TileRaw<D>& cur, const int kb, const int klim) {
         sm_sc[wave][lane] = cur.sc;
         __builtin_amdgcn_wave_barrier();
         // S^T = K Q^T, two 16-key halves.
@@ -266,10 +375,10 @@ __global__ __launch_bounds__(kDecThreads) void flash_decode_kernel(
             x[r]     = s[0][r] * (kf0[r] * scale_log2);
             x[4 + r] = s[1][r] * (kf1[r] * scale_log2);
         }
-        if (kb + kTileKeys > k1) {  // ragged last tile of the split
+        if (kb + kTileKeys > klim) {  // ragged last tile of the split
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
-                if (kb + key_of(g, j) >= k1) {
+                if (kb + key_of(g, j) >= klim) {
                     x[j] = -INFINITY;
                 }
             }
@@ -352,7 +461,7 @@ __global__ __launch_bounds__(kDecThreads) void flash_decode_kernel(
                     load_tile<D>(ring[(r + kRing - 1) % kRing], k, v, ks, vs,
                                  k0 + min(tr + (kRing - 1) * t_step, last_tile) * kTileKeys,
                                  k1, kvh, hkv, lane);
-                    process(ring[r], k0 + tr * kTileKeys);
+                    process(ring[r], k0 + tr * kTileKeys, k1);
                     done = tr + t_step > last_tile;
                 }
             }
@@ -360,6 +469,15 @@ __global__ __launch_bounds__(kDecThreads) void flash_decode_kernel(
                 break;
             }
         }
+    }
+
+    if (kAppend && virt) {
+        TileRaw<D>    vt;
+        const int64_t row = static_cast<int64_t>(p_new) * hkv + kvh;
+        quantize_new_token<D>(vt, k_new + static_cast<int64_t>(kvh) * D,
+                              v_new + static_cast<int64_t>(kvh) * D, k_w + row * D,
+                              v_w + row * D, ks_w + row, vs_w + row, lane);
+        process(vt, p_new, p_new + 1);
     }
 
     // ---- partial of this split, reference layout: m at [h*S + si] (log2
@@ -552,12 +670,21 @@ template <int D>
 hipError_t launch_decode(uint16_t* out, const uint16_t* q, const uint8_t* k,
                          const uint8_t* v, const float* ks, const float* vs,
                          float* partial, int num_splits, const int* cache_len,
-                         int hq, int hkv, float scale, hipStream_t stream) {
+                         int hq, int hkv, float scale, const uint16_t* k_new,
+                         const uint16_t* v_new, uint8_t* k_w, uint8_t* v_w, float* ks_w,
+                         float* vs_w, hipStream_t stream) {
     const int  n_wgs = dec_workgroups(num_splits, hkv);
     const dim3 grid(static_cast<unsigned>(n_wgs));
-    hipLaunchKernelGGL(flash_decode_kernel<D>, grid, dim3(kDecThreads), 0, stream,
-                       q, k, v, ks, vs, partial, num_splits, cache_len, hq, hkv,
-                       scale * kLog2e);
+    if (k_new != nullptr) {
+        hipLaunchKernelGGL((flash_decode_kernel<D, true>), grid, dim3(kDecThreads), 0, stream,
+                           q, k, v, ks, vs, partial, num_splits, cache_len, hq, hkv,
+                           scale * kLog2e, k_new, v_new, k_w, v_w, ks_w, vs_w);
+    } else {
+        hipLaunchKernelGGL((flash_decode_kernel<D, false>), grid, dim3(kDecThreads), 0, stream,
+                           q, k, v, ks, vs, partial, num_splits, cache_len, hq, hkv,
+                           scale * kLog2e, nullptr, nullptr, nullptr, nullptr, nullptr,
+                           nullptr);
+    }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) {
         return e;
@@ -589,17 +716,19 @@ hipError_t flash_decode_launch(uint16_t* out, const uint16_t* q,
                                float* partial, int num_splits,
                                const int* cache_len, int num_q_heads,
                                int num_kv_heads, int head_dim, float scale,
-                               hipStream_t stream) {
+                               hipStream_t stream, const uint16_t* k_new,
+                               const uint16_t* v_new, uint8_t* k_w, uint8_t* v_w,
+                               float* ks_w, float* vs_w) {
     switch (head_dim) {
-        case 64:
-            return launch_decode<64>(out, q, k, v, k_scale, v_scale, partial, num_splits,
-                                     cache_len, num_q_heads, num_kv_heads, scale, stream);
-        case 128:
-            return launch_decode<128>(out, q, k, v, k_scale, v_scale, partial, num_splits,
-                                      cache_len, num_q_heads, num_kv_heads, scale, stream);
-        case 256:
-            return launch_decode<256>(out, q, k, v, k_scale, v_scale, partial, num_splits,
-                                      cache_len, num_q_heads, num_kv_heads, scale, stream);
+#define RTH_DEC_CASE(DD)                                                                    \
+    case DD:                                                                                \
+        return launch_decode<DD>(out, q, k, v, k_scale, v_scale, partial, num_splits,       \
+                                 cache_len, num_q_heads, num_kv_heads, scale, k_new, v_new, \
+                                 k_w, v_w, ks_w, vs_w, stream);
+        RTH_DEC_CASE(64)
+        RTH_DEC_CASE(128)
+        RTH_DEC_CASE(256)
+#undef RTH_DEC_CASE
         default:
             return hipErrorInvalidValue;
     }

@@ -28,13 +28,19 @@ hipError_t kv_append_fp8_launch(uint8_t* k_q, uint8_t* v_q, float* k_scale,
 // Split-K decode scratch in floats: [Hq, S] m, [Hq, S] l, [Hq, S, D] acc.
 std::size_t decode_scratch_floats(int num_q_heads, int head_dim, int max_splits);
 
+// k_new != nullptr: also append one token (k_new, v_new [Hkv, D] bf16) at row
+// *cache_len of the cache (k_w, v_w, ks_w, vs_w: the same slabs as k, v,
+// k_scale, v_scale) before attending over *cache_len + 1 keys.
 hipError_t flash_decode_launch(uint16_t* out, const uint16_t* q,
                                const uint8_t* k, const uint8_t* v,
                                const float* k_scale, const float* v_scale,
                                float* partial, int num_splits,
                                const int* cache_len, int num_q_heads,
                                int num_kv_heads, int head_dim, float scale,
-                               hipStream_t stream);
+                               hipStream_t stream, const uint16_t* k_new = nullptr,
+                               const uint16_t* v_new = nullptr, uint8_t* k_w = nullptr,
+                               uint8_t* v_w = nullptr, float* ks_w = nullptr,
+                               float* vs_w = nullptr);
 
 hipError_t flash_prefill_launch(uint16_t* out, const uint16_t* q,
                                 const uint8_t* k, const uint8_t* v,

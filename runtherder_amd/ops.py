@@ -87,6 +87,21 @@ def flash_decode_split_bf16(out, q, k, v, k_scale, v_scale, partial, num_splits,
               num_kv_heads, head_dim, float(scale), _stream(stream))
 
 
+def flash_decode_append_split_bf16(out, q, k_cache, v_cache, k_scale, v_scale, k_new, v_new,
+                                   partial, num_splits, cache_len, num_q_heads, num_kv_heads,
+                                   head_dim, scale, stream=None):
+    """Append one token at row *cache_len and decode over *cache_len + 1 keys
+    in one call (no reference counterpart: KVCache::append then the decode)."""
+    _need(out, torch.bfloat16, "out"); _need(q, torch.bfloat16, "q")
+    _need(k_cache, torch.uint8, "k_cache"); _need(v_cache, torch.uint8, "v_cache")
+    _need(k_scale, torch.float32, "k_scale"); _need(v_scale, torch.float32, "v_scale")
+    _need(k_new, torch.bfloat16, "k_new"); _need(v_new, torch.bfloat16, "v_new")
+    _need(partial, torch.float32, "partial"); _need(cache_len, torch.int32, "cache_len")
+    _ffi.call("rth_attn_decode_append_split", _p(out), _p(q), _p(k_cache), _p(v_cache),
+              _p(k_scale), _p(v_scale), _p(k_new), _p(v_new), _p(partial), num_splits,
+              _p(cache_len), num_q_heads, num_kv_heads, head_dim, float(scale), _stream(stream))
+
+
 def flash_prefill_bf16(out, q, k, v, k_scale, v_scale, n_new, cache_len, num_q_heads,
                        num_kv_heads, head_dim, scale, stream=None):
     """reference include/runtherder/kernels/flash_prefill.cuh:26-39"""
@@ -284,6 +299,14 @@ class AdaptiveAttention(AttentionBackend):
         else:
             flash_prefill_bf16(out, q, kv.k, kv.v, kv.k_scale, kv.v_scale, n_new, cache_len,
                                c.num_q_heads, c.num_kv_heads, c.head_dim, c.scale, stream)
+
+    def run_decode_append(self, out, q, kv, k_new, v_new, cache_len, stream=None):
+        """KVCache.append(layer, k_new, v_new, 1, cache_len) + run(..., n_new=1)
+        in one call (the view's slabs receive the new token)."""
+        c = self.config
+        flash_decode_append_split_bf16(out, q, kv.k, kv.v, kv.k_scale, kv.v_scale, k_new, v_new,
+                                       self.partial, self.num_splits, cache_len, c.num_q_heads,
+                                       c.num_kv_heads, c.head_dim, c.scale, stream)
 
 
 class NaiveAttention(AttentionBackend):

@@ -157,3 +157,47 @@ def test_score_dynamic_range(splits):
     got = gpu_decode(q, k8, v8, ks, vs, total - 1, hq, hkv, d, splits, scale)
     assert np.isfinite(O.bf16_to_f32(got)).all()
     check(got, q, k8, v8, ks, vs, total - 1, hq, hkv, d, scale)
+
+
+@pytest.mark.parametrize("cache_len,hq,hkv,d,splits", [
+    (0, 24, 8, 128, None), (1, 24, 8, 128, None), (31, 24, 8, 128, None), (32, 24, 8, 128, None),
+    (2040, 24, 8, 128, None), (8195, 24, 8, 128, None), (9000, 32, 8, 128, 64),
+    (130, 8, 2, 64, 8), (700, 8, 4, 256, 16), (77, 64, 4, 128, 4), (40, 8, 2, 32, 4),
+])
+def test_decode_append_fused(cache_len, hq, hkv, d, splits):
+    """Fused append + decode: the cache row equals the append kernel's bytes
+    and the output matches the oracle (and the two-call sequence) within the
+    attention tolerance."""
+    scale = np.float32(1.0 / np.sqrt(d))
+    total = cache_len + 1
+    splits = splits or R.default_num_splits(hkv)
+    _, _, k8, v8, ks, vs = make_cache(total, hkv, d, kind="normal", seed=cache_len)
+    kn = O.normal_bf16((hkv, d), 3000 + cache_len)
+    vn = O.normal_bf16((hkv, d), 4000 + cache_len)
+    q = O.normal_bf16((hq, d), 5000 + cache_len)
+    rows = slice(cache_len * hkv, total * hkv)
+    k8[rows] = 0
+    v8[rows] = 0
+    kc, vc, ksd, vsd = u8_dev(k8), u8_dev(v8), f32_dev(ks), f32_dev(vs)
+    out = torch.empty((hq, d), dtype=torch.bfloat16, device=DEV)
+    partial = R.new_flash_split_scratch(hq, d, splits)
+    step(f"decode+append ctx={total} hq={hq} hkv={hkv} d={d} splits={splits}")
+    R.flash_decode_append_split_bf16(out, bf16_dev(q), kc, vc, ksd, vsd, bf16_dev(kn),
+                                     bf16_dev(vn), partial, splits, int_dev(cache_len), hq, hkv,
+                                     d, scale)
+    sync()
+    wk, wks = O.quantize_kv_fp8(kn, d)
+    wv, wvs = O.quantize_kv_fp8(vn, d)
+    gk, gv = kc.cpu().numpy(), vc.cpu().numpy()
+    gks, gvs = ksd.cpu().numpy(), vsd.cpu().numpy()
+    assert np.array_equal(gk[rows], wk) and np.array_equal(gv[rows], wv)
+    assert np.array_equal(gks[rows].view(np.uint32), wks.view(np.uint32))
+    assert np.array_equal(gvs[rows].view(np.uint32), wvs.view(np.uint32))
+    others = np.ones(total * hkv, bool)
+    others[rows] = False
+    assert np.array_equal(gk[others], k8[others]) and np.array_equal(gks[others], ks[others])
+    got = bf16_host(out)
+    check(got, q, gk, gv, gks, gvs, cache_len, hq, hkv, d, scale)
+    two = gpu_decode(q, gk, gv, gks, gvs, cache_len, hq, hkv, d, splits, scale)
+    mx, mean = O.bf16_err(got, two)
+    assert mx <= MAX_ABS and mean <= 1e-3, (mx, mean)
