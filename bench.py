@@ -90,36 +90,44 @@ def bench_decode(torch, R, args, stream):
         pos.fill_(depth)
     torch.cuda.synchronize()
 
-    def run_steps():
+    def run_steps(fused):
         for s in range(GRAPH_STEPS):
             for l in range(L):
-                cache.append(l, ks[s, l], vs[s, l], 1, pos)
-                backend.run(out[s, l], qs[s, l], cache.view(l), 1, pos)
+                if fused:
+                    backend.run_decode_append(out[s, l], qs[s, l], cache.view(l), ks[s, l],
+                                              vs[s, l], pos)
+                else:
+                    cache.append(l, ks[s, l], vs[s, l], 1, pos)
+                    backend.run(out[s, l], qs[s, l], cache.view(l), 1, pos)
             R.advance_position(pos, 1)
         R.advance_position(pos, -GRAPH_STEPS)   # replays are idempotent
 
-    graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph, stream=stream):
-        run_steps()
-    torch.cuda.synchronize()
-
     replays_w = max(1, math.ceil(args.warmup / GRAPH_STEPS))
     replays = max(1, math.ceil(args.steps / GRAPH_STEPS))
-    with torch.cuda.stream(stream):
-        for _ in range(replays_w):
-            graph.replay()
-    torch.cuda.synchronize()
-    with torch.cuda.stream(stream):
-        with EventTimer(torch, stream) as t:
-            for _ in range(replays):
-                graph.replay()
-    torch.cuda.synchronize()
-    steps = replays * GRAPH_STEPS
-    ms_per_step = t.ms / steps
     step_bytes = [sum(decode_bytes(ctx0 + s, hq, hkv, d) for _ in range(L))
                   for s in range(GRAPH_STEPS)]
     total_bytes = replays * sum(step_bytes)
-    value_gbs = total_bytes / (t.ms * 1e-3) / 1e9
+    timed = {}
+    for fused in (False, True):
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=stream):
+            run_steps(fused)
+        torch.cuda.synchronize()
+        with torch.cuda.stream(stream):
+            for _ in range(replays_w):
+                graph.replay()
+        torch.cuda.synchronize()
+        with torch.cuda.stream(stream):
+            with EventTimer(torch, stream) as t:
+                for _ in range(replays):
+                    graph.replay()
+        torch.cuda.synchronize()
+        timed[fused] = t.ms
+        del graph
+    steps = replays * GRAPH_STEPS
+    ms_per_step = timed[True] / steps
+    value_gbs = total_bytes / (timed[True] * 1e-3) / 1e9
+    unfused_gbs = total_bytes / (timed[False] * 1e-3) / 1e9
 
     # Dominant kernels alone: one decode call (split kernel + merge kernel) per
     # layer, rotating over the 28 layers (defeats the 256 MB Infinity Cache),
@@ -143,6 +151,7 @@ def bench_decode(torch, R, args, stream):
     achieved = kbytes / (kern_us * 1e-6) / 1e9
     return {
         "value": value_gbs, "ms_per_step": ms_per_step, "steps": steps,
+        "unfused_value": unfused_gbs, "unfused_ms_per_step": timed[False] / steps,
         "warmup": replays_w * GRAPH_STEPS, "ctx": ctx0, "splits": backend.num_splits,
         "kernel_us": kern_us, "kernel_bytes": kbytes, "kernel_gbs": achieved,
         "cache": cache, "qs": qs, "depth": depth, "hq": hq, "hkv": hkv, "d": d,
@@ -446,7 +455,8 @@ def main() -> int:
         "data": "synthetic: N(0,1) bf16 q/k/v, k/v quantized to FP8 E4M3 by the append kernel",
         "config": {
             "workload": "config3: 28-layer Llama-3.2-3B-shaped decode attention, 24Q/8KV, "
-                        "head_dim 128, ctx 8196..8323, per layer append+split-K decode, "
+                        "head_dim 128, ctx 8196..8323, per layer one-token K/V append + "
+                        "split-K decode through the fused append+decode entry (2 kernels), "
                         "128 steps per HIP graph",
             "ctx": dec["ctx"], "layers": 28, "num_splits": dec["splits"],
             "parallelism": "single GPU",
@@ -472,6 +482,12 @@ def main() -> int:
         "rope_append": dict(ra, workload="config4 shapes: RoPE(q,k) + K/V FP8 append (and the "
                                          "Qwen3 q/k RMSNorm before it), fused entries vs the "
                                          "unfused launch sequences"),
+        "decode_step_unfused": {
+            "value": round(dec["unfused_value"], 1), "unit": "GB/s",
+            "ms_per_step": round(dec["unfused_ms_per_step"], 4),
+            "workload": "the same steps as KVCache.append then AdaptiveAttention.run (3 kernels "
+                        "per layer, the reference's call sequence)",
+        },
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
