@@ -154,6 +154,37 @@ int rth_rope_append_fp8(uint16_t* q, uint8_t* k_cache, uint8_t* v_cache,
                         int num_q_heads, int num_kv_heads, int head_dim,
                         void* stream);
 
+/* Paged KV cache (no counterpart in the reference, whose README plans paged
+ * attention; SURVEY next item 3): the cache slabs hold physical blocks of
+ * block_size positions ([num_blocks * block_size, Hkv, D] E4M3 and
+ * [num_blocks * block_size, Hkv] fp32 scales); logical position p of the
+ * sequence lives at physical position block_table[p / block_size] *
+ * block_size + p % block_size. block_table is a device int array covering
+ * every block up to the last position used; block_size is a power of two
+ * >= 32. Each entry below equals its contiguous counterpart on the gathered
+ * cache, bit for bit. */
+int rth_kv_append_fp8_paged(uint8_t* k_cache, uint8_t* v_cache, float* k_scale,
+                            float* v_scale, const uint16_t* k, const uint16_t* v,
+                            const int* at_pos, int n_new, int num_kv_heads, int head_dim,
+                            const int* block_table, int block_size, void* stream);
+int rth_attn_decode_split_paged(uint16_t* out, const uint16_t* q, const uint8_t* k,
+                                const uint8_t* v, const float* k_scale, const float* v_scale,
+                                const int* block_table, int block_size, float* partial,
+                                int num_splits, const int* cache_len, int num_q_heads,
+                                int num_kv_heads, int head_dim, float scale, void* stream);
+int rth_attn_decode_append_split_paged(uint16_t* out, const uint16_t* q, uint8_t* k_cache,
+                                       uint8_t* v_cache, float* k_scale, float* v_scale,
+                                       const int* block_table, int block_size,
+                                       const uint16_t* k_new, const uint16_t* v_new,
+                                       float* partial, int num_splits, const int* cache_len,
+                                       int num_q_heads, int num_kv_heads, int head_dim,
+                                       float scale, void* stream);
+int rth_attn_prefill_paged(uint16_t* out, const uint16_t* q, const uint8_t* k,
+                           const uint8_t* v, const float* k_scale, const float* v_scale,
+                           const int* block_table, int block_size, int n_new,
+                           const int* cache_len, int num_q_heads, int num_kv_heads,
+                           int head_dim, float scale, void* stream);
+
 /* No counterpart in the reference: fuses the Qwen3 caller sequence
  * rmsnorm_bf16_forward(q, q_norm) [per q head], rmsnorm_bf16_forward(k,
  * k_norm) [per kv head], rope_bf16(q, k), KVCache::append(k, v) (reference

@@ -13,6 +13,12 @@ struct KVView {
     const __hip_fp8_e4m3* v;
     const float*          k_scale;
     const float*          v_scale;
+    // Paged layout (no reference counterpart; the reference README plans
+    // paged attention): when block_table is set, position p lives at row
+    // block_table[p / block_size] * block_size + p % block_size of the slabs.
+    // Views built as KVView{k, v, k_scale, v_scale} stay contiguous.
+    const int* block_table = nullptr;
+    int        block_size  = 0;
 };
 
 }  // namespace runtherder::attention

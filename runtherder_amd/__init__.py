@@ -15,6 +15,7 @@ from .ops import (  # noqa: F401
     KVCache,
     KVView,
     NaiveAttention,
+    PagedKVCache,
     advance_position,
     attention_causal_bf16,
     default_num_splits,

@@ -39,6 +39,16 @@ _SIGNATURES = {
                                              _c_int, _c_int, _vp]),
     "rth_rmsnorm_bf16": (_c_int, [_vp, _vp, _vp, _c_int, _c_int, ctypes.c_float, _vp]),
     "rth_rmsnorm_lanes": (_c_int, [_c_int]),
+    "rth_kv_append_fp8_paged": (_c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_int, _c_int,
+                                         _c_int, _vp, _c_int, _vp]),
+    "rth_attn_decode_split_paged": (_c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_int, _vp,
+                                             _c_int, _vp, _c_int, _c_int, _c_int,
+                                             ctypes.c_float, _vp]),
+    "rth_attn_decode_append_split_paged": (_c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_int,
+                                                    _vp, _vp, _vp, _c_int, _vp, _c_int, _c_int,
+                                                    _c_int, ctypes.c_float, _vp]),
+    "rth_attn_prefill_paged": (_c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_int, _c_int, _vp,
+                                        _c_int, _c_int, _c_int, ctypes.c_float, _vp]),
 }
 
 _lib: ctypes.CDLL | None = None

@@ -73,6 +73,24 @@ int check_attn(const void* out, const void* q, const void* k, const void* v,
     return RTH_OK;
 }
 
+// Paged caches: block_size a power of two >= 32 (a decode tile of 32 keys
+// never straddles a block); returns the block shift or -1.
+int block_shift_of(int block_size) {
+    if (block_size < 32 || (block_size & (block_size - 1)) != 0) {
+        return -1;
+    }
+    int sh = 0;
+    while ((1 << sh) < block_size) {
+        ++sh;
+    }
+    return sh;
+}
+
+#define RTH_PAGED_ARGS(bt, bs, shift)                                              \
+    RTH_REQUIRE((bt) != nullptr, "block_table must not be null");                  \
+    const int shift = block_shift_of(bs);                                          \
+    RTH_REQUIRE(shift >= 0, "block_size must be a power of two >= 32")
+
 }  // namespace
 
 extern "C" {
@@ -212,6 +230,97 @@ int rth_attn_decode_append_split(uint16_t* out, const uint16_t* q, uint8_t* k_ca
                                                  cache_len, num_q_heads, num_kv_heads,
                                                  head_dim, scale, as_stream(stream)),
                      "rth_attn_decode_append_split");
+}
+
+int rth_kv_append_fp8_paged(uint8_t* k_cache, uint8_t* v_cache, float* k_scale,
+                            float* v_scale, const uint16_t* k, const uint16_t* v,
+                            const int* at_pos, int n_new, int num_kv_heads, int head_dim,
+                            const int* block_table, int block_size, void* stream) {
+    RTH_REQUIRE(n_new >= 1, "KVCache append n_new must be >= 1");
+    RTH_REQUIRE(num_kv_heads >= 1, "num_kv_heads must be >= 1");
+    RTH_REQUIRE(k_cache != nullptr && v_cache != nullptr && k_scale != nullptr &&
+                    v_scale != nullptr && k != nullptr && v != nullptr,
+                "cache slabs, scales and inputs must not be null");
+    RTH_PAGED_ARGS(block_table, block_size, shift);
+    if (int rc = check_quant(k_cache, k_scale, k, at_pos, num_kv_heads,
+                             n_new * num_kv_heads, head_dim)) {
+        return rc;
+    }
+    return check_hip(rth::kv_append_fp8_launch(k_cache, v_cache, k_scale, v_scale, k, v,
+                                               at_pos, num_kv_heads, n_new * num_kv_heads,
+                                               head_dim, as_stream(stream), block_table, shift),
+                     "rth_kv_append_fp8_paged");
+}
+
+int rth_attn_decode_split_paged(uint16_t* out, const uint16_t* q, const uint8_t* k,
+                                const uint8_t* v, const float* k_scale, const float* v_scale,
+                                const int* block_table, int block_size, float* partial,
+                                int num_splits, const int* cache_len, int num_q_heads,
+                                int num_kv_heads, int head_dim, float scale, void* stream) {
+    if (int rc = check_attn(out, q, k, v, k_scale, v_scale, cache_len)) {
+        return rc;
+    }
+    RTH_PAGED_ARGS(block_table, block_size, shift);
+    RTH_REQUIRE(num_splits >= 1, "num_splits must be >= 1");
+    if (int rc = check_heads(num_q_heads, num_kv_heads)) {
+        return rc;
+    }
+    RTH_REQUIRE(rth::decode_mfma_supported(num_q_heads, num_kv_heads, head_dim),
+                "paged decode supports head_dim 64, 128, 256 with Hq/Hkv <= 16");
+    RTH_REQUIRE(partial != nullptr, "partial must not be null");
+    return check_hip(rth::flash_decode_launch(out, q, k, v, k_scale, v_scale, partial,
+                                              num_splits, cache_len, num_q_heads, num_kv_heads,
+                                              head_dim, scale, as_stream(stream), nullptr,
+                                              nullptr, nullptr, nullptr, nullptr, nullptr,
+                                              block_table, shift),
+                     "rth_attn_decode_split_paged");
+}
+
+int rth_attn_decode_append_split_paged(uint16_t* out, const uint16_t* q, uint8_t* k_cache,
+                                       uint8_t* v_cache, float* k_scale, float* v_scale,
+                                       const int* block_table, int block_size,
+                                       const uint16_t* k_new, const uint16_t* v_new,
+                                       float* partial, int num_splits, const int* cache_len,
+                                       int num_q_heads, int num_kv_heads, int head_dim,
+                                       float scale, void* stream) {
+    if (int rc = check_attn(out, q, k_cache, v_cache, k_scale, v_scale, cache_len)) {
+        return rc;
+    }
+    RTH_PAGED_ARGS(block_table, block_size, shift);
+    RTH_REQUIRE(k_new != nullptr && v_new != nullptr, "k_new and v_new must not be null");
+    RTH_REQUIRE(num_splits >= 1, "num_splits must be >= 1");
+    if (int rc = check_heads(num_q_heads, num_kv_heads)) {
+        return rc;
+    }
+    RTH_REQUIRE(rth::decode_mfma_supported(num_q_heads, num_kv_heads, head_dim),
+                "paged decode supports head_dim 64, 128, 256 with Hq/Hkv <= 16");
+    RTH_REQUIRE(partial != nullptr, "partial must not be null");
+    return check_hip(rth::flash_decode_launch(out, q, k_cache, v_cache, k_scale, v_scale,
+                                              partial, num_splits, cache_len, num_q_heads,
+                                              num_kv_heads, head_dim, scale, as_stream(stream),
+                                              k_new, v_new, k_cache, v_cache, k_scale, v_scale,
+                                              block_table, shift),
+                     "rth_attn_decode_append_split_paged");
+}
+
+int rth_attn_prefill_paged(uint16_t* out, const uint16_t* q, const uint8_t* k,
+                           const uint8_t* v, const float* k_scale, const float* v_scale,
+                           const int* block_table, int block_size, int n_new,
+                           const int* cache_len, int num_q_heads, int num_kv_heads,
+                           int head_dim, float scale, void* stream) {
+    if (int rc = check_attn(out, q, k, v, k_scale, v_scale, cache_len)) {
+        return rc;
+    }
+    RTH_PAGED_ARGS(block_table, block_size, shift);
+    RTH_REQUIRE(head_dim == 128, "flash_prefill_bf16 supports head_dim 128 only");
+    RTH_REQUIRE(n_new >= 1, "n_new must be >= 1");
+    if (int rc = check_heads(num_q_heads, num_kv_heads)) {
+        return rc;
+    }
+    return check_hip(rth::flash_prefill_launch(out, q, k, v, k_scale, v_scale, n_new, cache_len,
+                                               num_q_heads, num_kv_heads, head_dim, scale,
+                                               as_stream(stream), block_table, shift),
+                     "rth_attn_prefill_paged");
 }
 
 int rth_attn_prefill(uint16_t* out, const uint16_t* q, const uint8_t* k,

@@ -65,6 +65,17 @@ struct DecTraits {
     static constexpr int kRing    = 2;  // register tiles in flight (deeper measured slower)
 };
 
+// Physical cache row of logical key `key` when the cache is paged: blocks of
+// 2^block_shift keys, logical block b stored at physical block
+// block_table[b]. A 32-key tile never straddles a block (blocks hold a
+// multiple of 32 keys and tiles start at multiples of 32), so one lookup per
+// tile gives the tile's offset `delta` (physical - logical key).
+__device__ __forceinline__ int paged_row(int key, const int* __restrict__ block_table,
+                                         int block_shift) {
+    const int mask = (1 << block_shift) - 1;
+    return (block_table[key >> block_shift] << block_shift) | (key & mask);
+}
+
 // One tile's raw global data held by a lane.
 template <int D>
 struct TileRaw {
@@ -82,14 +93,14 @@ __device__ __forceinline__ void load_tile(TileRaw<D>& t, const uint8_t* __restri
                                           const uint8_t* __restrict__ v,
                                           const float* __restrict__ ks,
                                           const float* __restrict__ vs, int kb,
-                                          int k1, int kvh, int hkv, int lane) {
+                                          int k1, int kvh, int hkv, int lane, int delta) {
     using T     = DecTraits<D>;
     const int n = lane & 15;
     const int g = lane >> 4;
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
         const int      key = min(kb + 16 * u + n, k1 - 1);
-        const uint8_t* kr  = k + (static_cast<int64_t>(key) * hkv + kvh) * D;
+        const uint8_t* kr  = k + (static_cast<int64_t>(key + delta) * hkv + kvh) * D;
 #pragma unroll
         for (int c = 0; c < T::kKChunks; ++c) {
             t.kraw[u][c] = *reinterpret_cast<const u32x4*>(kr + 16 * g + 64 * c);
@@ -98,7 +109,7 @@ __device__ __forceinline__ void load_tile(TileRaw<D>& t, const uint8_t* __restri
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
         const int      key = min(kb + key_of(g, j), k1 - 1);
-        const uint8_t* vr  = v + (static_cast<int64_t>(key) * hkv + kvh) * D + T::kVBytes * n;
+        const uint8_t* vr  = v + (static_cast<int64_t>(key + delta) * hkv + kvh) * D + T::kVBytes * n;
         if constexpr (T::kVWords == 1) {
             t.vraw[j][0] = *reinterpret_cast<const uint32_t*>(vr);
         } else if constexpr (T::kVWords == 2) {
@@ -115,7 +126,7 @@ __device__ __forceinline__ void load_tile(TileRaw<D>& t, const uint8_t* __restri
     }
     {
         const int     key = min(kb + (lane & 31), k1 - 1);
-        const int64_t row = static_cast<int64_t>(key) * hkv + kvh;
+        const int64_t row = static_cast<int64_t>(key + delta) * hkv + kvh;
         t.sc              = (lane < 32) ? ks[row] : vs[row];
     }
 }
@@ -255,14 +266,16 @@ __device__ __forceinline__ void quantize_new_token(TileRaw<D>& vt, const uint16_
 // row *cache_len of the cache; the unit whose split holds that key quantizes
 // it, stores codes and scales, and attends to it from registers, so no wave
 // reads the row being written.
-template <int D, bool kAppend>
+// kPaged: K/V/scale rows are addressed through block_table (see paged_row).
+template <int D, bool kAppend, bool kPaged>
 __global__ __launch_bounds__(kDecThreads) void flash_decode_kernel(
     const uint16_t* __restrict__ q, const uint8_t* __restrict__ k,
     const uint8_t* __restrict__ v, const float* __restrict__ ks,
     const float* __restrict__ vs, float* __restrict__ partial, int num_splits,
     const int* __restrict__ cache_len, int hq, int hkv, float scale_log2,
     const uint16_t* __restrict__ k_new, const uint16_t* __restrict__ v_new,
-    uint8_t* k_w, uint8_t* v_w, float* ks_w, float* vs_w) {
+    uint8_t* k_w, uint8_t* v_w, float* ks_w, float* vs_w,
+    const int* __restrict__ block_table, int block_shift) {
     using T = DecTraits<D>;
 
     __shared__ __attribute__((aligned(16))) float sm_sc[kDecWaves][64];
@@ -446,11 +459,17 @@ __global__ __launch_bounds__(kDecThreads) void flash_decode_kernel(
     const int     last_tile = n_tiles - 1;
     if (t_first <= last_tile) {
         TileRaw<D> ring[kRing];
+        auto tile_delta = [&](int kb) {
+            if constexpr (kPaged) {
+                return paged_row(kb, block_table, block_shift) - kb;
+            } else {
+                return 0;
+            }
+        };
 #pragma unroll
         for (int r = 0; r + 1 < kRing; ++r) {
-            load_tile<D>(ring[r], k, v, ks, vs,
-                         k0 + min(t_first + r * t_step, last_tile) * kTileKeys, k1, kvh, hkv,
-                         lane);
+            const int kb = k0 + min(t_first + r * t_step, last_tile) * kTileKeys;
+            load_tile<D>(ring[r], k, v, ks, vs, kb, k1, kvh, hkv, lane, tile_delta(kb));
         }
         for (int t = t_first;; t += kRing * t_step) {
             bool done = false;
@@ -458,9 +477,9 @@ __global__ __launch_bounds__(kDecThreads) void flash_decode_kernel(
             for (int r = 0; r < kRing; ++r) {
                 if (!done) {
                     const int tr = t + r * t_step;
-                    load_tile<D>(ring[(r + kRing - 1) % kRing], k, v, ks, vs,
-                                 k0 + min(tr + (kRing - 1) * t_step, last_tile) * kTileKeys,
-                                 k1, kvh, hkv, lane);
+                    const int kbn = k0 + min(tr + (kRing - 1) * t_step, last_tile) * kTileKeys;
+                    load_tile<D>(ring[(r + kRing - 1) % kRing], k, v, ks, vs, kbn, k1, kvh, hkv,
+                                 lane, tile_delta(kbn));
                     process(ring[r], k0 + tr * kTileKeys, k1);
                     done = tr + t_step > last_tile;
                 }
@@ -473,7 +492,8 @@ __global__ __launch_bounds__(kDecThreads) void flash_decode_kernel(
 
     if (kAppend && virt) {
         TileRaw<D>    vt;
-        const int64_t row = static_cast<int64_t>(p_new) * hkv + kvh;
+        const int     prow = kPaged ? paged_row(p_new, block_table, block_shift) : p_new;
+        const int64_t row  = static_cast<int64_t>(prow) * hkv + kvh;
         quantize_new_token<D>(vt, k_new + static_cast<int64_t>(kvh) * D,
                               v_new + static_cast<int64_t>(kvh) * D, k_w + row * D,
                               v_w + row * D, ks_w + row, vs_w + row, lane);
@@ -666,24 +686,26 @@ __global__ void advance_position_kernel(int* pos, int delta) {
     }
 }
 
-template <int D>
+template <int D, bool kPaged>
 hipError_t launch_decode(uint16_t* out, const uint16_t* q, const uint8_t* k,
                          const uint8_t* v, const float* ks, const float* vs,
                          float* partial, int num_splits, const int* cache_len,
                          int hq, int hkv, float scale, const uint16_t* k_new,
                          const uint16_t* v_new, uint8_t* k_w, uint8_t* v_w, float* ks_w,
-                         float* vs_w, hipStream_t stream) {
+                         float* vs_w, const int* block_table, int block_shift,
+                         hipStream_t stream) {
     const int  n_wgs = dec_workgroups(num_splits, hkv);
     const dim3 grid(static_cast<unsigned>(n_wgs));
     if (k_new != nullptr) {
-        hipLaunchKernelGGL((flash_decode_kernel<D, true>), grid, dim3(kDecThreads), 0, stream,
-                           q, k, v, ks, vs, partial, num_splits, cache_len, hq, hkv,
-                           scale * kLog2e, k_new, v_new, k_w, v_w, ks_w, vs_w);
+        hipLaunchKernelGGL((flash_decode_kernel<D, true, kPaged>), grid, dim3(kDecThreads), 0,
+                           stream, q, k, v, ks, vs, partial, num_splits, cache_len, hq, hkv,
+                           scale * kLog2e, k_new, v_new, k_w, v_w, ks_w, vs_w, block_table,
+                           block_shift);
     } else {
-        hipLaunchKernelGGL((flash_decode_kernel<D, false>), grid, dim3(kDecThreads), 0, stream,
-                           q, k, v, ks, vs, partial, num_splits, cache_len, hq, hkv,
-                           scale * kLog2e, nullptr, nullptr, nullptr, nullptr, nullptr,
-                           nullptr);
+        hipLaunchKernelGGL((flash_decode_kernel<D, false, kPaged>), grid, dim3(kDecThreads), 0,
+                           stream, q, k, v, ks, vs, partial, num_splits, cache_len, hq, hkv,
+                           scale * kLog2e, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr,
+                           block_table, block_shift);
     }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) {
@@ -718,13 +740,20 @@ hipError_t flash_decode_launch(uint16_t* out, const uint16_t* q,
                                int num_kv_heads, int head_dim, float scale,
                                hipStream_t stream, const uint16_t* k_new,
                                const uint16_t* v_new, uint8_t* k_w, uint8_t* v_w,
-                               float* ks_w, float* vs_w) {
+                               float* ks_w, float* vs_w, const int* block_table,
+                               int block_shift) {
+    const bool paged = block_table != nullptr;
     switch (head_dim) {
-#define RTH_DEC_CASE(DD)                                                                    \
-    case DD:                                                                                \
-        return launch_decode<DD>(out, q, k, v, k_scale, v_scale, partial, num_splits,       \
-                                 cache_len, num_q_heads, num_kv_heads, scale, k_new, v_new, \
-                                 k_w, v_w, ks_w, vs_w, stream);
+#define RTH_DEC_CASE(DD)                                                                      \
+    case DD:                                                                                  \
+        return paged ? launch_decode<DD, true>(out, q, k, v, k_scale, v_scale, partial,       \
+                                               num_splits, cache_len, num_q_heads,            \
+                                               num_kv_heads, scale, k_new, v_new, k_w, v_w,   \
+                                               ks_w, vs_w, block_table, block_shift, stream)  \
+                     : launch_decode<DD, false>(out, q, k, v, k_scale, v_scale, partial,      \
+                                                num_splits, cache_len, num_q_heads,           \
+                                                num_kv_heads, scale, k_new, v_new, k_w, v_w,  \
+                                                ks_w, vs_w, nullptr, 0, stream);
         RTH_DEC_CASE(64)
         RTH_DEC_CASE(128)
         RTH_DEC_CASE(256)

@@ -55,13 +55,28 @@ struct PfRaw {
     float sc;     // k_scale or v_scale of one key
 };
 
+// Physical cache row of logical key `key` (identity unless paged: blocks of
+// 2^block_shift keys, logical block b at physical block block_table[b]).
+template <bool kPaged>
+__device__ __forceinline__ int pf_row(int key, const int* __restrict__ block_table,
+                                      int block_shift) {
+    if constexpr (kPaged) {
+        return (block_table[key >> block_shift] << block_shift) |
+               (key & ((1 << block_shift) - 1));
+    } else {
+        return key;
+    }
+}
+
+template <bool kPaged>
 __device__ __forceinline__ void pf_load(PfRaw& r, const uint8_t* __restrict__ k,
                                         const uint8_t* __restrict__ v,
                                         const float* __restrict__ ks,
                                         const float* __restrict__ vs, int key0,
-                                        int total, int kvh, int hkv, int tid) {
+                                        int total, int kvh, int hkv, int tid,
+                                        const int* __restrict__ bt, int bshift) {
     {
-        const int      key = min(key0 + (tid >> 2), total - 1);
+        const int      key = pf_row<kPaged>(min(key0 + (tid >> 2), total - 1), bt, bshift);
         const uint8_t* kr  = k + (static_cast<int64_t>(key) * hkv + kvh) * kHD + 32 * (tid & 3);
         r.k[0] = *reinterpret_cast<const u32x4*>(kr);
         r.k[1] = *reinterpret_cast<const u32x4*>(kr + 16);
@@ -71,13 +86,13 @@ __device__ __forceinline__ void pf_load(PfRaw& r, const uint8_t* __restrict__ k,
         const int d0 = 8 * (tid >> 4);     // 8 d of those 4 keys
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            const int key = min(key0 + 4 * kq + j, total - 1);
+            const int key = pf_row<kPaged>(min(key0 + 4 * kq + j, total - 1), bt, bshift);
             r.v[j] = *reinterpret_cast<const u32x2*>(
                 v + (static_cast<int64_t>(key) * hkv + kvh) * kHD + d0);
         }
     }
     if (tid < 2 * kBN) {
-        const int     key = min(key0 + (tid & (kBN - 1)), total - 1);
+        const int     key = pf_row<kPaged>(min(key0 + (tid & (kBN - 1)), total - 1), bt, bshift);
         const int64_t row = static_cast<int64_t>(key) * hkv + kvh;
         r.sc = (tid < kBN) ? ks[row] : vs[row];
     }
@@ -134,11 +149,13 @@ __device__ __forceinline__ void pf_stage(const PfRaw& r, uint16_t* sK, uint16_t*
     }
 }
 
+template <bool kPaged>
 __global__ __launch_bounds__(kPfThreads, 2) void flash_prefill_kernel(
     uint16_t* __restrict__ out, const uint16_t* __restrict__ q,
     const uint8_t* __restrict__ k, const uint8_t* __restrict__ v,
     const float* __restrict__ ks, const float* __restrict__ vs, int n_new,
-    const int* __restrict__ cache_len, int hq, int hkv, float scale_log2) {
+    const int* __restrict__ cache_len, int hq, int hkv, float scale_log2,
+    const int* __restrict__ block_table, int block_shift) {
     __shared__ __attribute__((aligned(16))) uint16_t sK[kBN * kKPitch];
     __shared__ __attribute__((aligned(16))) uint16_t sVt[kHD * kVPitch];
     __shared__ __attribute__((aligned(16))) float    sKf[kBN];
@@ -195,14 +212,15 @@ __global__ __launch_bounds__(kPfThreads, 2) void flash_prefill_kernel(
     float l_run = 0.0f;
 
     PfRaw raw;
-    pf_load(raw, k, v, ks, vs, 0, total, kvh, hkv, tid);
+    pf_load<kPaged>(raw, k, v, ks, vs, 0, total, kvh, hkv, tid, block_table, block_shift);
 
     for (int kt = 0; kt < n_tiles; ++kt) {
         __syncthreads();
         pf_stage(raw, sK, sVt, sKf, sVf, tid, scale_log2);
         __syncthreads();
         if (kt + 1 < n_tiles) {
-            pf_load(raw, k, v, ks, vs, (kt + 1) * kBN, total, kvh, hkv, tid);
+            pf_load<kPaged>(raw, k, v, ks, vs, (kt + 1) * kBN, total, kvh, hkv, tid, block_table,
+                            block_shift);
         }
         if (kt >= w_tiles) {
             continue;
@@ -380,15 +398,22 @@ hipError_t flash_prefill_launch(uint16_t* out, const uint16_t* q,
                                 const float* k_scale, const float* v_scale,
                                 int n_new, const int* cache_len,
                                 int num_q_heads, int num_kv_heads,
-                                int head_dim, float scale, hipStream_t stream) {
+                                int head_dim, float scale, hipStream_t stream,
+                                const int* block_table, int block_shift) {
     if (head_dim != kHD) {
         return hipErrorInvalidValue;
     }
     const int  n_blk = (n_new + kBM - 1) / kBM;
     const dim3 grid(static_cast<unsigned>(n_blk * num_q_heads));
-    hipLaunchKernelGGL(flash_prefill_kernel, grid, dim3(kPfThreads), 0, stream, out, q,
-                       k, v, k_scale, v_scale, n_new, cache_len, num_q_heads,
-                       num_kv_heads, scale * kLog2e);
+    if (block_table != nullptr) {
+        hipLaunchKernelGGL(flash_prefill_kernel<true>, grid, dim3(kPfThreads), 0, stream, out, q,
+                           k, v, k_scale, v_scale, n_new, cache_len, num_q_heads, num_kv_heads,
+                           scale * kLog2e, block_table, block_shift);
+    } else {
+        hipLaunchKernelGGL(flash_prefill_kernel<false>, grid, dim3(kPfThreads), 0, stream, out,
+                           q, k, v, k_scale, v_scale, n_new, cache_len, num_q_heads,
+                           num_kv_heads, scale * kLog2e, nullptr, 0);
+    }
     return hipGetLastError();
 }
 

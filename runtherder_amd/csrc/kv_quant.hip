@@ -28,10 +28,14 @@ struct QuantSlab {
 };
 
 // Mode 0: scale from the row amax. Mode 1: scale given at the destination row.
-template <int kLanesPerRow, int kMode>
+// kPaged: destination position p = *at_pos + row / rows_per_pos is stored at
+// physical position (block_table[p >> block_shift] << block_shift) |
+// (p & (2^block_shift - 1)).
+template <int kLanesPerRow, int kMode, bool kPaged>
 __global__ __launch_bounds__(kQuantBlock) void quantize_rows_kernel(
     QuantSlab s0, QuantSlab s1, const int* __restrict__ at_pos,
-    int rows_per_pos, int num_rows, int head_dim) {
+    int rows_per_pos, int num_rows, int head_dim, const int* __restrict__ block_table,
+    int block_shift) {
     const QuantSlab s       = (blockIdx.y == 0) ? s0 : s1;
     constexpr int   kRowsPB = kQuantBlock / kLanesPerRow;
     const int       sub     = static_cast<int>(threadIdx.x) % kLanesPerRow;
@@ -40,8 +44,15 @@ __global__ __launch_bounds__(kQuantBlock) void quantize_rows_kernel(
     const bool      live    = row < num_rows;
     const int       n_vec   = head_dim / 8;
 
-    const int64_t dst = static_cast<int64_t>(row) +
-                        static_cast<int64_t>(*at_pos) * rows_per_pos;
+    int64_t dst;
+    if constexpr (kPaged) {
+        const int p    = *at_pos + row / rows_per_pos;
+        const int phys = (live ? (block_table[p >> block_shift] << block_shift) : 0) |
+                         (p & ((1 << block_shift) - 1));
+        dst = static_cast<int64_t>(phys) * rows_per_pos + row % rows_per_pos;
+    } else {
+        dst = static_cast<int64_t>(row) + static_cast<int64_t>(*at_pos) * rows_per_pos;
+    }
     const uint16_t* xr = s.x + static_cast<int64_t>(row) * head_dim;
 
     u32x4 cache[kMaxCached];
@@ -117,10 +128,11 @@ __global__ __launch_bounds__(kQuantBlock) void quantize_rows_kernel(
     }
 }
 
-template <int kMode>
+template <int kMode, bool kPaged>
 hipError_t launch_quant(QuantSlab s0, QuantSlab s1, int n_slabs,
                         const int* at_pos, int rows_per_pos, int num_rows,
-                        int head_dim, hipStream_t stream) {
+                        int head_dim, const int* block_table, int block_shift,
+                        hipStream_t stream) {
     const int n_vec = head_dim / 8;
     int       lpr   = 1;
     while (lpr < n_vec && lpr < kWave) {
@@ -130,11 +142,11 @@ hipError_t launch_quant(QuantSlab s0, QuantSlab s1, int n_slabs,
     const dim3 grid(static_cast<unsigned>((num_rows + rows_pb - 1) / rows_pb),
                     static_cast<unsigned>(n_slabs));
     switch (lpr) {
-#define RTH_Q_CASE(L)                                                              \
-    case L:                                                                        \
-        hipLaunchKernelGGL((quantize_rows_kernel<L, kMode>), grid, dim3(kQuantBlock), \
-                           0, stream, s0, s1, at_pos, rows_per_pos, num_rows,      \
-                           head_dim);                                              \
+#define RTH_Q_CASE(L)                                                                    \
+    case L:                                                                              \
+        hipLaunchKernelGGL((quantize_rows_kernel<L, kMode, kPaged>), grid,               \
+                           dim3(kQuantBlock), 0, stream, s0, s1, at_pos, rows_per_pos,   \
+                           num_rows, head_dim, block_table, block_shift);                \
         break;
         RTH_Q_CASE(1)
         RTH_Q_CASE(2)
@@ -156,7 +168,8 @@ hipError_t quantize_kv_fp8_launch(uint8_t* q, float* scale, const uint16_t* x,
                                   const int* at_pos, int rows_per_pos,
                                   int num_rows, int head_dim, hipStream_t stream) {
     const QuantSlab s{q, scale, x};
-    return launch_quant<0>(s, s, 1, at_pos, rows_per_pos, num_rows, head_dim, stream);
+    return launch_quant<0, false>(s, s, 1, at_pos, rows_per_pos, num_rows, head_dim, nullptr, 0,
+                                  stream);
 }
 
 hipError_t quantize_kv_fp8_scaled_launch(uint8_t* q, const float* scale,
@@ -164,17 +177,23 @@ hipError_t quantize_kv_fp8_scaled_launch(uint8_t* q, const float* scale,
                                          int rows_per_pos, int num_rows,
                                          int head_dim, hipStream_t stream) {
     const QuantSlab s{q, const_cast<float*>(scale), x};
-    return launch_quant<1>(s, s, 1, at_pos, rows_per_pos, num_rows, head_dim, stream);
+    return launch_quant<1, false>(s, s, 1, at_pos, rows_per_pos, num_rows, head_dim, nullptr, 0,
+                                  stream);
 }
 
 hipError_t kv_append_fp8_launch(uint8_t* k_q, uint8_t* v_q, float* k_scale,
                                 float* v_scale, const uint16_t* k,
                                 const uint16_t* v, const int* at_pos,
                                 int rows_per_pos, int num_rows, int head_dim,
-                                hipStream_t stream) {
+                                hipStream_t stream, const int* block_table, int block_shift) {
     const QuantSlab sk{k_q, k_scale, k};
     const QuantSlab sv{v_q, v_scale, v};
-    return launch_quant<0>(sk, sv, 2, at_pos, rows_per_pos, num_rows, head_dim, stream);
+    if (block_table != nullptr) {
+        return launch_quant<0, true>(sk, sv, 2, at_pos, rows_per_pos, num_rows, head_dim,
+                                     block_table, block_shift, stream);
+    }
+    return launch_quant<0, false>(sk, sv, 2, at_pos, rows_per_pos, num_rows, head_dim, nullptr,
+                                  0, stream);
 }
 
 }  // namespace rth

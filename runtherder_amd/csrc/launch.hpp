@@ -19,11 +19,13 @@ hipError_t quantize_kv_fp8_scaled_launch(uint8_t* q, const float* scale,
                                          int rows_per_pos, int num_rows,
                                          int head_dim, hipStream_t stream);
 
+// block_table != nullptr: paged cache (see flash_prefill_launch).
 hipError_t kv_append_fp8_launch(uint8_t* k_q, uint8_t* v_q, float* k_scale,
                                 float* v_scale, const uint16_t* k,
                                 const uint16_t* v, const int* at_pos,
                                 int rows_per_pos, int num_rows, int head_dim,
-                                hipStream_t stream);
+                                hipStream_t stream, const int* block_table = nullptr,
+                                int block_shift = 0);
 
 // Split-K decode scratch in floats: [Hq, S] m, [Hq, S] l, [Hq, S, D] acc.
 std::size_t decode_scratch_floats(int num_q_heads, int head_dim, int max_splits);
@@ -40,14 +42,18 @@ hipError_t flash_decode_launch(uint16_t* out, const uint16_t* q,
                                hipStream_t stream, const uint16_t* k_new = nullptr,
                                const uint16_t* v_new = nullptr, uint8_t* k_w = nullptr,
                                uint8_t* v_w = nullptr, float* ks_w = nullptr,
-                               float* vs_w = nullptr);
+                               float* vs_w = nullptr, const int* block_table = nullptr,
+                               int block_shift = 0);
 
+// block_table != nullptr: paged cache, logical block b (2^block_shift keys)
+// stored at physical block block_table[b] (same for the decode launch).
 hipError_t flash_prefill_launch(uint16_t* out, const uint16_t* q,
                                 const uint8_t* k, const uint8_t* v,
                                 const float* k_scale, const float* v_scale,
                                 int n_new, const int* cache_len,
                                 int num_q_heads, int num_kv_heads,
-                                int head_dim, float scale, hipStream_t stream);
+                                int head_dim, float scale, hipStream_t stream,
+                                const int* block_table = nullptr, int block_shift = 0);
 
 hipError_t attention_naive_launch(uint16_t* out, const uint16_t* q,
                                   const uint8_t* k, const uint8_t* v,

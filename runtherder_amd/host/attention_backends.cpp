@@ -40,11 +40,25 @@ void AdaptiveAttention::run(__hip_bfloat16* out, const __hip_bfloat16* q, const 
     auto* qq = reinterpret_cast<const std::uint16_t*>(q);
     auto* k  = reinterpret_cast<const std::uint8_t*>(kv.k);
     auto* v  = reinterpret_cast<const std::uint8_t*>(kv.v);
+    const bool paged = kv.block_table != nullptr;
     if (n_new == 1) {
-        RUNTHERDER_RTH_CHECK(rth_attn_decode_split(o, qq, k, v, kv.k_scale, kv.v_scale,
-                                                   partial_.get(), num_splits_, cache_len,
-                                                   config_.num_q_heads, config_.num_kv_heads,
-                                                   config_.head_dim, config_.scale, stream));
+        if (paged) {
+            RUNTHERDER_RTH_CHECK(rth_attn_decode_split_paged(
+                o, qq, k, v, kv.k_scale, kv.v_scale, kv.block_table, kv.block_size,
+                partial_.get(), num_splits_, cache_len, config_.num_q_heads,
+                config_.num_kv_heads, config_.head_dim, config_.scale, stream));
+        } else {
+            RUNTHERDER_RTH_CHECK(rth_attn_decode_split(o, qq, k, v, kv.k_scale, kv.v_scale,
+                                                       partial_.get(), num_splits_, cache_len,
+                                                       config_.num_q_heads, config_.num_kv_heads,
+                                                       config_.head_dim, config_.scale, stream));
+        }
+        return;
+    }
+    if (paged) {
+        RUNTHERDER_RTH_CHECK(rth_attn_prefill_paged(
+            o, qq, k, v, kv.k_scale, kv.v_scale, kv.block_table, kv.block_size, n_new, cache_len,
+            config_.num_q_heads, config_.num_kv_heads, config_.head_dim, config_.scale, stream));
         return;
     }
     RUNTHERDER_RTH_CHECK(rth_attn_prefill(o, qq, k, v, kv.k_scale, kv.v_scale, n_new, cache_len,
@@ -56,6 +70,7 @@ NaiveAttention::NaiveAttention(const AttnConfig& config) noexcept : config_(conf
 
 void NaiveAttention::run(__hip_bfloat16* out, const __hip_bfloat16* q, const KVView& kv,
                          int n_new, const int* cache_len, hipStream_t stream) {
+    RUNTHERDER_CHECK(kv.block_table == nullptr, "NaiveAttention reads contiguous caches only");
     RUNTHERDER_RTH_CHECK(rth_attn_naive(
         reinterpret_cast<std::uint16_t*>(out), reinterpret_cast<const std::uint16_t*>(q),
         reinterpret_cast<const std::uint8_t*>(kv.k), reinterpret_cast<const std::uint8_t*>(kv.v),

@@ -205,11 +205,14 @@ class AttnConfig:
 
 @dataclass(frozen=True)
 class KVView:
-    """reference include/runtherder/attention/kv_view.h:14-19"""
+    """reference include/runtherder/attention/kv_view.h:14-19; block_table /
+    block_size (no reference counterpart) describe a paged layout."""
     k: torch.Tensor
     v: torch.Tensor
     k_scale: torch.Tensor
     v_scale: torch.Tensor
+    block_table: torch.Tensor | None = None
+    block_size: int = 0
 
 
 class KVCache:
@@ -271,6 +274,43 @@ class KVCache:
         return self._max_seq_len
 
 
+class PagedKVCache:
+    """Paged FP8 KV cache: per layer num_blocks physical blocks of block_size
+    positions; the caller's block_table (int32 device tensor, logical block ->
+    physical block) goes to append() and view(). No reference counterpart."""
+
+    def __init__(self, num_layers, num_blocks, block_size, num_kv_heads, head_dim,
+                 device="cuda"):
+        if block_size < 32 or block_size & (block_size - 1):
+            raise ValueError("PagedKVCache block_size must be a power of two >= 32")
+        self.num_layers, self.num_blocks, self.block_size = num_layers, num_blocks, block_size
+        self.num_kv_heads, self.head_dim = num_kv_heads, head_dim
+        shape = (num_layers, num_blocks * block_size, num_kv_heads, head_dim)
+        self.k = torch.empty(shape, dtype=torch.uint8, device=device)
+        self.v = torch.empty(shape, dtype=torch.uint8, device=device)
+        self.k_scale = torch.empty(shape[:3], dtype=torch.float32, device=device)
+        self.v_scale = torch.empty(shape[:3], dtype=torch.float32, device=device)
+
+    def append(self, layer, k, v, n_new, at_pos, block_table, stream=None):
+        if not 0 <= layer < self.num_layers:
+            raise ValueError("KVCache append layer out of range")
+        if n_new < 1:
+            raise ValueError("KVCache append n_new must be >= 1")
+        _need(k, torch.bfloat16, "k"); _need(v, torch.bfloat16, "v")
+        _need(at_pos, torch.int32, "at_pos"); _need(block_table, torch.int32, "block_table")
+        _ffi.call("rth_kv_append_fp8_paged", _p(self.k[layer]), _p(self.v[layer]),
+                  _p(self.k_scale[layer]), _p(self.v_scale[layer]), _p(k), _p(v), _p(at_pos),
+                  n_new, self.num_kv_heads, self.head_dim, _p(block_table), self.block_size,
+                  _stream(stream))
+
+    def view(self, layer, block_table) -> KVView:
+        if not 0 <= layer < self.num_layers:
+            raise ValueError("KVCache view layer out of range")
+        _need(block_table, torch.int32, "block_table")
+        return KVView(self.k[layer], self.v[layer], self.k_scale[layer], self.v_scale[layer],
+                      block_table, self.block_size)
+
+
 class AttentionBackend:
     """reference include/runtherder/attention/backend.h:24-53"""
 
@@ -292,6 +332,18 @@ class AdaptiveAttention(AttentionBackend):
 
     def run(self, out, q, kv, n_new, cache_len, stream=None):
         c = self.config
+        if kv.block_table is not None:
+            if n_new == 1:
+                _ffi.call("rth_attn_decode_split_paged", _p(out), _p(q), _p(kv.k), _p(kv.v),
+                          _p(kv.k_scale), _p(kv.v_scale), _p(kv.block_table), kv.block_size,
+                          _p(self.partial), self.num_splits, _p(cache_len), c.num_q_heads,
+                          c.num_kv_heads, c.head_dim, float(c.scale), _stream(stream))
+            else:
+                _ffi.call("rth_attn_prefill_paged", _p(out), _p(q), _p(kv.k), _p(kv.v),
+                          _p(kv.k_scale), _p(kv.v_scale), _p(kv.block_table), kv.block_size,
+                          n_new, _p(cache_len), c.num_q_heads, c.num_kv_heads, c.head_dim,
+                          float(c.scale), _stream(stream))
+            return
         if n_new == 1:
             flash_decode_split_bf16(out, q, kv.k, kv.v, kv.k_scale, kv.v_scale, self.partial,
                                     self.num_splits, cache_len, c.num_q_heads, c.num_kv_heads,
@@ -304,6 +356,13 @@ class AdaptiveAttention(AttentionBackend):
         """KVCache.append(layer, k_new, v_new, 1, cache_len) + run(..., n_new=1)
         in one call (the view's slabs receive the new token)."""
         c = self.config
+        if kv.block_table is not None:
+            _ffi.call("rth_attn_decode_append_split_paged", _p(out), _p(q), _p(kv.k), _p(kv.v),
+                      _p(kv.k_scale), _p(kv.v_scale), _p(kv.block_table), kv.block_size,
+                      _p(k_new), _p(v_new), _p(self.partial), self.num_splits, _p(cache_len),
+                      c.num_q_heads, c.num_kv_heads, c.head_dim, float(c.scale),
+                      _stream(stream))
+            return
         flash_decode_append_split_bf16(out, q, kv.k, kv.v, kv.k_scale, kv.v_scale, k_new, v_new,
                                        self.partial, self.num_splits, cache_len, c.num_q_heads,
                                        c.num_kv_heads, c.head_dim, c.scale, stream)
@@ -316,6 +375,8 @@ class NaiveAttention(AttentionBackend):
         self.config = config
 
     def run(self, out, q, kv, n_new, cache_len, stream=None):
+        if kv.block_table is not None:
+            raise ValueError("NaiveAttention reads contiguous caches only")
         c = self.config
         attention_causal_bf16(out, q, kv.k, kv.v, kv.k_scale, kv.v_scale, n_new, cache_len,
                               c.num_q_heads, c.num_kv_heads, c.head_dim, c.scale, stream)

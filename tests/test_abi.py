@@ -81,13 +81,16 @@ def test_cpp_headers_compile():
 #include <runtherder/attention/adaptive.h>
 #include <runtherder/attention/naive.h>
 #include <runtherder/engine/kv_cache.h>
+#include <runtherder/engine/paged_kv_cache.h>
 #include <runtherder/kernels/quantization.h>
 #include <runtherder/kernels/flash_decode.h>
 #include <runtherder/kernels/flash_prefill.h>
 #include <runtherder/kernels/attention.h>
 #include <runtherder/kernels/rope.h>
 #include <runtherder/kernels/rmsnorm.h>
-static_assert(sizeof(runtherder::attention::KVView) == 4 * sizeof(void*));
+static_assert(sizeof(runtherder::attention::KVView) == 6 * sizeof(void*));
+// The reference's aggregate form still builds a contiguous view.
+static_assert(runtherder::attention::KVView{nullptr, nullptr, nullptr, nullptr}.block_table == nullptr);
 int main() { return 0; }
 """
     res = subprocess.run(["/opt/rocm/bin/hipcc", "-std=c++20", "-fsyntax-only", "-x", "hip",
@@ -114,3 +117,14 @@ def test_rmsnorm_rejects_and_lanes():
                             FAKE, None, FAKE, ctypes.c_float(1e-6), FAKE, FAKE, FAKE, 4, 32, 8,
                             128, None)
     assert [R.rmsnorm_lanes(d) for d in (8, 64, 128, 256, 4096, 12)] == [1, 8, 16, 32, 64, 0]
+
+
+def test_paged_rejects_block_sizes():
+    for bs in (16, 48, 0):
+        assert "power of two" in _err("rth_attn_prefill_paged", FAKE, FAKE, FAKE, FAKE, FAKE, FAKE,
+                                      FAKE, bs, 4, FAKE, 32, 8, 128, ctypes.c_float(0.1), None)
+    assert "block_table" in _err("rth_attn_decode_split_paged", FAKE, FAKE, FAKE, FAKE, FAKE,
+                                 FAKE, None, 64, FAKE, 4, FAKE, 32, 8, 128, ctypes.c_float(0.1),
+                                 None)
+    assert "power of two" in _err("rth_kv_append_fp8_paged", FAKE, FAKE, FAKE, FAKE, FAKE, FAKE,
+                                  FAKE, 4, 8, 128, FAKE, 100, None)
