@@ -75,8 +75,17 @@ __device__ __forceinline__ void pf_load(PfRaw& r, const uint8_t* __restrict__ k,
                                         const float* __restrict__ vs, int key0,
                                         int total, int kvh, int hkv, int tid,
                                         const int* __restrict__ bt, int bshift) {
+    // Paged: the tile's two 32-key halves each lie inside one block (blocks
+    // hold a power of two >= 32 keys), so two uniform lookups give the
+    // physical offsets; clamped keys stay inside the tile.
+    int d_lo = 0, d_hi = 0;
+    if constexpr (kPaged) {
+        d_lo = pf_row<true>(key0, bt, bshift) - key0;
+        d_hi = (key0 + 32 < total) ? pf_row<true>(key0 + 32, bt, bshift) - (key0 + 32) : d_lo;
+    }
+    auto phys = [&](int key) { return key + ((key - key0 < 32) ? d_lo : d_hi); };
     {
-        const int      key = pf_row<kPaged>(min(key0 + (tid >> 2), total - 1), bt, bshift);
+        const int      key = phys(min(key0 + (tid >> 2), total - 1));
         const uint8_t* kr  = k + (static_cast<int64_t>(key) * hkv + kvh) * kHD + 32 * (tid & 3);
         r.k[0] = *reinterpret_cast<const u32x4*>(kr);
         r.k[1] = *reinterpret_cast<const u32x4*>(kr + 16);
@@ -86,13 +95,13 @@ __device__ __forceinline__ void pf_load(PfRaw& r, const uint8_t* __restrict__ k,
         const int d0 = 8 * (tid >> 4);     // 8 d of those 4 keys
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            const int key = pf_row<kPaged>(min(key0 + 4 * kq + j, total - 1), bt, bshift);
+            const int key = phys(min(key0 + 4 * kq + j, total - 1));
             r.v[j] = *reinterpret_cast<const u32x2*>(
                 v + (static_cast<int64_t>(key) * hkv + kvh) * kHD + d0);
         }
     }
     if (tid < 2 * kBN) {
-        const int     key = pf_row<kPaged>(min(key0 + (tid & (kBN - 1)), total - 1), bt, bshift);
+        const int     key = phys(min(key0 + (tid & (kBN - 1)), total - 1));
         const int64_t row = static_cast<int64_t>(key) * hkv + kvh;
         r.sc = (tid < kBN) ? ks[row] : vs[row];
     }
