@@ -7,7 +7,8 @@
 //
 // MI355X design:
 //  * Workgroup = one q head x 128 query rows, 4 waves of 32 rows. Grid order
-//    puts the longest (last) row blocks first and keeps the q heads of one kv
+//    puts the longest (last) row blocks first (a grid resident in one round
+//    pairs them with the lightest instead) and keeps the q heads of one kv
 //    head on one XCD so their K/V tiles share an L2.
 //  * Each 64-key tile is staged in LDS as bf16 converted exactly from the E4M3
 //    codes: K row-major [key][d], V transposed [d][key] (the transpose is done
@@ -164,7 +165,7 @@ __global__ __launch_bounds__(kPfThreads, 2) void flash_prefill_kernel(
     const uint8_t* __restrict__ k, const uint8_t* __restrict__ v,
     const float* __restrict__ ks, const float* __restrict__ vs, int n_new,
     const int* __restrict__ cache_len, int hq, int hkv, float scale_log2,
-    const int* __restrict__ block_table, int block_shift) {
+    const int* __restrict__ block_table, int block_shift, bool one_round) {
     __shared__ __attribute__((aligned(16))) uint16_t sK[kBN * kKPitch];
     __shared__ __attribute__((aligned(16))) uint16_t sVt[kHD * kVPitch];
     __shared__ __attribute__((aligned(16))) float    sKf[kBN];
@@ -177,9 +178,14 @@ __global__ __launch_bounds__(kPfThreads, 2) void flash_prefill_kernel(
     const int h    = lane >> 5;   // k-group
 
     // Block mapping: heavy row blocks first; q heads of one kv head on one XCD.
-    const int n_blk = (n_new + kBM - 1) / kBM;
-    const int bid   = static_cast<int>(blockIdx.x);
-    const int blk   = n_blk - 1 - bid / hq;
+    // When the whole grid is resident at once (one_round), the second half of
+    // the grid runs the light blocks in ascending order, so the two
+    // workgroups sharing a compute unit pair a heavy block with a light one.
+    const int n_blk    = (n_new + kBM - 1) / kBM;
+    const int bid      = static_cast<int>(blockIdx.x);
+    const int half_wgs = (n_blk / 2) * hq;
+    const int blk      = (one_round && bid >= half_wgs) ? (bid - half_wgs) / hq
+                                                        : n_blk - 1 - bid / hq;
     const int hb    = bid % hq;
     const int qh    = ((hq & 7) == 0) ? ((hb & 7) * (hq >> 3) + (hb >> 3)) : hb;
     const int G     = hq / hkv;
@@ -414,14 +420,21 @@ hipError_t flash_prefill_launch(uint16_t* out, const uint16_t* q,
     }
     const int  n_blk = (n_new + kBM - 1) / kBM;
     const dim3 grid(static_cast<unsigned>(n_blk * num_q_heads));
+    // Two workgroups fit per compute unit (LDS and registers).
+    int dev = 0, cus = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) {
+        cus = 0;
+    }
+    const bool one_round = n_blk * num_q_heads <= 2 * cus;
     if (block_table != nullptr) {
         hipLaunchKernelGGL(flash_prefill_kernel<true>, grid, dim3(kPfThreads), 0, stream, out, q,
                            k, v, k_scale, v_scale, n_new, cache_len, num_q_heads, num_kv_heads,
-                           scale * kLog2e, block_table, block_shift);
+                           scale * kLog2e, block_table, block_shift, one_round);
     } else {
         hipLaunchKernelGGL(flash_prefill_kernel<false>, grid, dim3(kPfThreads), 0, stream, out,
                            q, k, v, k_scale, v_scale, n_new, cache_len, num_q_heads,
-                           num_kv_heads, scale * kLog2e, nullptr, 0);
+                           num_kv_heads, scale * kLog2e, nullptr, 0, one_round);
     }
     return hipGetLastError();
 }
