@@ -172,7 +172,7 @@ int rth_attn_decode_split(uint16_t* out, const uint16_t* q, const uint8_t* k,
     if (int rc = check_attn(out, q, k, v, k_scale, v_scale, cache_len)) {
         return rc;
     }
-    RTH_REQUIRE(num_splits >= 1, "num_splits must be >= 1");
+    RTH_REQUIRE(num_splits >= 1 && num_splits <= 65536, "num_splits must be in [1, 65536]");
     if (int rc = check_heads(num_q_heads, num_kv_heads)) {
         return rc;
     }
@@ -203,7 +203,7 @@ int rth_attn_decode_append_split(uint16_t* out, const uint16_t* q, uint8_t* k_ca
         return rc;
     }
     RTH_REQUIRE(k_new != nullptr && v_new != nullptr, "k_new and v_new must not be null");
-    RTH_REQUIRE(num_splits >= 1, "num_splits must be >= 1");
+    RTH_REQUIRE(num_splits >= 1 && num_splits <= 65536, "num_splits must be in [1, 65536]");
     if (int rc = check_heads(num_q_heads, num_kv_heads)) {
         return rc;
     }
@@ -261,7 +261,7 @@ int rth_attn_decode_split_paged(uint16_t* out, const uint16_t* q, const uint8_t*
         return rc;
     }
     RTH_PAGED_ARGS(block_table, block_size, shift);
-    RTH_REQUIRE(num_splits >= 1, "num_splits must be >= 1");
+    RTH_REQUIRE(num_splits >= 1 && num_splits <= 65536, "num_splits must be in [1, 65536]");
     if (int rc = check_heads(num_q_heads, num_kv_heads)) {
         return rc;
     }
@@ -288,7 +288,7 @@ int rth_attn_decode_append_split_paged(uint16_t* out, const uint16_t* q, uint8_t
     }
     RTH_PAGED_ARGS(block_table, block_size, shift);
     RTH_REQUIRE(k_new != nullptr && v_new != nullptr, "k_new and v_new must not be null");
-    RTH_REQUIRE(num_splits >= 1, "num_splits must be >= 1");
+    RTH_REQUIRE(num_splits >= 1 && num_splits <= 65536, "num_splits must be in [1, 65536]");
     if (int rc = check_heads(num_q_heads, num_kv_heads)) {
         return rc;
     }

@@ -55,6 +55,11 @@ def test_decode_rejects_gqa_ratio_and_null():
                               FAKE, 4, FAKE, 32, 8, 96, ctypes.c_float(0.1), None)
 
 
+def test_decode_rejects_split_count_overflow():
+    assert "65536" in _err("rth_attn_decode_split", FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE,
+                           1 << 20, FAKE, 32, 8, 128, ctypes.c_float(0.1), None)
+
+
 def test_quantize_rejects_bad_rows():
     assert "divisible by 8" in _err("rth_kv_quantize_fp8", FAKE, FAKE, FAKE, FAKE, 1, 4, 12, None)
     assert "at_pos" in _err("rth_kv_quantize_fp8", FAKE, FAKE, FAKE, None, 1, 4, 128, None)
