@@ -159,7 +159,9 @@ def bench_decode(torch, R, args, stream):
     }
 
 
-def bench_prefill(torch, R, stream, n=4096, iters=10):
+def bench_prefill(torch, R, stream, n=4096, iters=None):
+    """Prefill calls timed back to back after ~30 ms of warmup calls (the
+    clock settles under the MFMA load), over ~60 ms unless iters is given."""
     hq, hkv, d = 32, 8, 128
     scale = 1.0 / math.sqrt(d)
     dev = torch.device("cuda:0")
@@ -174,7 +176,12 @@ def bench_prefill(torch, R, stream, n=4096, iters=10):
         out = torch.empty((n, hq, d), dtype=torch.bfloat16, device=dev)
         view = cache.view(0)
         cache.append(0, k, v, n, pos)
-        for _ in range(3):
+        fl = prefill_flops(n, 0, hq, d)
+        call_s = fl / 0.9e15                  # ~ one call at 900 TFLOP/s
+        warm = max(3, int(0.03 / call_s))
+        if iters is None:
+            iters = max(5, int(0.06 / call_s))
+        for _ in range(warm):
             R.flash_prefill_bf16(out, q, view.k, view.v, view.k_scale, view.v_scale, n, pos,
                                  hq, hkv, d, scale)
         torch.cuda.synchronize()
@@ -296,7 +303,7 @@ def decode_kernel_sweep(torch, R, stream, points):
 def prefill_sweep(torch, R, stream, ns):
     out = []
     for n in ns:
-        pf = bench_prefill(torch, R, stream, n=n, iters=5 if n > 8192 else 10)
+        pf = bench_prefill(torch, R, stream, n=n)
         out.append({"n": n, "us": round(pf["us"], 1), "tflops": round(pf["tflops"], 1),
                     "frac": round(pf["tflops"] / PEAK_BF16_TFLOPS, 4)})
         print(json.dumps({"prefill_sweep": out[-1]}), flush=True)

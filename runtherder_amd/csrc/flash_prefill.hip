@@ -1,4 +1,4 @@
-// Causal flash prefill over an OCP E4M3 KV cache on bf16 MFMA, gfx950.
+// Causal flash prefill over an OCP E4M3 KV cache, gfx950.
 //
 // Math follows flash_prefill_bf16 (reference src/kernels/flash_prefill.cu:
 // 34-241): causal rule "query t at position cache_len + t sees keys
@@ -6,39 +6,43 @@
 // O / l. head_dim is 128, as in the reference (:226).
 //
 // MI355X design:
-//  * Workgroup = one q head x 128 query rows, 4 waves of 32 rows. Grid order
-//    puts the longest (last) row blocks first (a grid resident in one round
-//    pairs them with the lightest instead) and keeps the q heads of one kv
-//    head on one XCD so their K/V tiles share an L2.
-//  * Each 64-key tile is staged in LDS as bf16 converted exactly from the E4M3
-//    codes: K row-major [key][d], V transposed [d][key] (the transpose is done
-//    in registers with v_perm before the LDS write). Row pitches are padded by
-//    16 bytes so the 128-bit MFMA operand reads are bank-conflict free. The next
-//    tile's global loads are issued before the current tile's MFMAs.
-//  * Scores are computed transposed, S^T = K Q^T with
-//    v_mfma_f32_32x32x16_bf16 (A = K from LDS, B = Q^T held in registers), so
-//    each lane owns one query row: the softmax max/sum need one cross-lane
-//    step and the O^T rescale is a per-lane scalar. P^T feeds O^T += V^T P^T
-//    straight from the score registers (the V^T LDS columns are stored in the
-//    matching key order).
-//  * The per-(token, kv_head) scales stay in fp32: k_scale * softmax_scale *
-//    log2(e) multiplies each score column, v_scale multiplies P before its
-//    bf16 rounding. The softmax runs in base 2.
-//  * Tiles beyond a wave's last query position are skipped per wave; masking
-//    is evaluated only on tiles that cross the diagonal or the key end.
+//  * Workgroup = one q head x (32 x waves) query rows, 32 rows per wave; the
+//    grid puts the longest (last) row blocks first and keeps the q heads of
+//    one kv head on one XCD so their K/V tiles share an L2.
+//  * Keys go in 64-key tiles. The K tile's E4M3 codes are copied unchanged
+//    into LDS by the LDS-DMA loads (global_load_lds_dwordx4, 16-byte chunks
+//    XOR-swizzled by row so the operand reads are bank-conflict free), one
+//    tile ahead, with no registers or VALU work.
+//  * Scores S^T = K Q^T run on the fp8 MFMA v_mfma_scale_f32_32x32x64_f8f6f4
+//    with A = the raw K codes from LDS and B = Q split exactly into two E4M3
+//    parts: q * 2^a = hi + lo / 16 (a per row, so the row maximum lands in
+//    [128, 256)), the MFMA's per-lane E8M0 scales undoing 2^a and 16. A bf16
+//    q has 8 significant bits and hi takes the top 4, so the split is exact
+//    and every product is the exact code * q product, accumulated in fp32 -
+//    the same scores as exact E4M3 codes times bf16 q.
+//  * Each lane owns one query row (the S^T column), so the softmax needs no
+//    cross-lane step except on a rebase. t = s * (k_scale * scale * log2 e)
+//    - m_ref against a lazy reference maximum; p = 2^t rounded to f16.
+//  * V is dequantized into LDS as f16(code * v_scale), transposed to V^T in
+//    registers (v_perm) before the LDS write, and O^T += V^T P^T runs on
+//    v_mfma_f32_32x32x16_f16 with P^T straight from the score registers.
+//  * Two buffers for K codes, k_scale factors and V^T: tile kt + 1 is loaded
+//    and staged while tile kt is consumed; one barrier per tile.
 #include "device_common.hpp"
 #include "launch.hpp"
 
 namespace rth {
 namespace {
 
-constexpr int kPfWaves   = 4;
-constexpr int kPfThreads = kPfWaves * kWave;
-constexpr int kBM        = 128;          // query rows per workgroup
-constexpr int kBN        = 64;           // keys per tile
-constexpr int kHD        = 128;          // head_dim
-constexpr int kKPitch    = kHD + 8;      // bf16 per K row in LDS   (272 B)
-constexpr int kVPitch    = kBN + 8;      // bf16 per V^T row in LDS (144 B)
+typedef int      i32x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+
+constexpr int kBN     = 64;          // keys per tile
+constexpr int kHD     = 128;         // head_dim
+constexpr int kKTile  = kBN * kHD;   // bytes of E4M3 K codes per tile
+constexpr int kVPitch = kBN + 8;     // f16 per V^T row in LDS (144 B)
+constexpr int kE8M0One = 127;        // E8M0 encoding of 1.0
 
 // LDS column of key o (0..63) in the V^T tile: within each group of 16 keys,
 // offset 8a + 4h + b is stored at 8h + 4a + b, so the 8 keys one MFMA lane
@@ -49,12 +53,6 @@ __device__ __forceinline__ int vt_pos(int o) {
     const int h   = (o >> 2) & 1;
     return grp + 8 * h + 4 * a + (o & 3);
 }
-
-struct PfRaw {
-    u32x4 k[2];   // 32 E4M3 bytes of one K row
-    u32x2 v[4];   // 8 E4M3 bytes (d0..d0+7) of 4 consecutive V rows
-    float sc;     // k_scale or v_scale of one key
-};
 
 // Physical cache row of logical key `key` (identity unless paged: blocks of
 // 2^block_shift keys, logical block b at physical block block_table[b]).
@@ -69,107 +67,155 @@ __device__ __forceinline__ int pf_row(int key, const int* __restrict__ block_tab
     }
 }
 
+// Physical row of key `key` of the tile starting at key0, clamped to the last
+// key. Paged: the tile's two 32-key halves each lie inside one block (blocks
+// hold a power of two >= 32 keys), so two uniform lookups per tile suffice.
 template <bool kPaged>
-__device__ __forceinline__ void pf_load(PfRaw& r, const uint8_t* __restrict__ k,
-                                        const uint8_t* __restrict__ v,
-                                        const float* __restrict__ ks,
-                                        const float* __restrict__ vs, int key0,
-                                        int total, int kvh, int hkv, int tid,
-                                        const int* __restrict__ bt, int bshift) {
-    // Paged: the tile's two 32-key halves each lie inside one block (blocks
-    // hold a power of two >= 32 keys), so two uniform lookups give the
-    // physical offsets; clamped keys stay inside the tile.
-    int d_lo = 0, d_hi = 0;
-    if constexpr (kPaged) {
-        d_lo = pf_row<true>(key0, bt, bshift) - key0;
-        d_hi = (key0 + 32 < total) ? pf_row<true>(key0 + 32, bt, bshift) - (key0 + 32) : d_lo;
-    }
-    auto phys = [&](int key) { return key + ((key - key0 < 32) ? d_lo : d_hi); };
-    {
-        const int      key = phys(min(key0 + (tid >> 2), total - 1));
-        const uint8_t* kr  = k + (static_cast<int64_t>(key) * hkv + kvh) * kHD + 32 * (tid & 3);
-        r.k[0] = *reinterpret_cast<const u32x4*>(kr);
-        r.k[1] = *reinterpret_cast<const u32x4*>(kr + 16);
-    }
-    {
-        const int kq = tid & 15;           // key quad 0..15
-        const int d0 = 8 * (tid >> 4);     // 8 d of those 4 keys
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int key = phys(min(key0 + 4 * kq + j, total - 1));
-            r.v[j] = *reinterpret_cast<const u32x2*>(
-                v + (static_cast<int64_t>(key) * hkv + kvh) * kHD + d0);
+struct TileRows {
+    int key0, total, d_lo, d_hi;
+    __device__ __forceinline__ TileRows(int key0_, int total_, const int* __restrict__ bt,
+                                        int bshift)
+        : key0(key0_), total(total_), d_lo(0), d_hi(0) {
+        if constexpr (kPaged) {
+            d_lo = pf_row<true>(key0, bt, bshift) - key0;
+            d_hi = (key0 + 32 < total) ? pf_row<true>(key0 + 32, bt, bshift) - (key0 + 32) : d_lo;
         }
     }
-    if (tid < 2 * kBN) {
-        const int     key = phys(min(key0 + (tid & (kBN - 1)), total - 1));
-        const int64_t row = static_cast<int64_t>(key) * hkv + kvh;
-        r.sc = (tid < kBN) ? ks[row] : vs[row];
+    __device__ __forceinline__ int operator()(int i) const {   // i = key offset in the tile
+        const int key = min(key0 + i, total - 1);
+        return key + ((key - key0 < 32) ? d_lo : d_hi);
+    }
+};
+
+// Byte offset of 16-byte chunk c (0..7) of K row r (0..63) in an LDS K tile.
+__device__ __forceinline__ int k_chunk(int r, int c) {
+    return r * kHD + 16 * (c ^ (r & 7));
+}
+
+// Issues the LDS-DMA copy of one K tile: slot s (16 bytes) holds chunk
+// (s & 7) ^ (row & 7) of row s >> 3, so that k_chunk() finds it.
+template <int kThreads, bool kPaged>
+__device__ __forceinline__ void k_tile_dma(uint8_t* dst, const uint8_t* __restrict__ k,
+                                           const TileRows<kPaged>& rows, int kvh, int hkv,
+                                           int tid) {
+#pragma unroll
+    for (int rep = 0; rep < kKTile / 16 / kThreads; ++rep) {
+        const int      s   = tid + rep * kThreads;
+        const int      r   = s >> 3;
+        const int      c   = (s & 7) ^ (r & 7);
+        const uint8_t* src = k + (static_cast<int64_t>(rows(r)) * hkv + kvh) * kHD + 16 * c;
+        // The destination base is wave-uniform; lane l lands at base + 16 l.
+        __builtin_amdgcn_global_load_lds(src, dst + 16 * (s & ~(kWave - 1)), 16, 0, 0);
     }
 }
 
-__device__ __forceinline__ void pf_stage(const PfRaw& r, uint16_t* sK, uint16_t* sVt,
-                                         float* sKf, float* sVf, int tid,
-                                         float scale_log2) {
-    {
-        const int row = tid >> 2;
-        const int c0  = 32 * (tid & 3);
-        bf16x8    a, b, c, d;
-        e4m3x16_to_bf16x8x2(r.k[0], a, b);
-        e4m3x16_to_bf16x8x2(r.k[1], c, d);
-        uint16_t* dst = sK + row * kKPitch + c0;
-        *reinterpret_cast<bf16x8*>(dst)      = a;
-        *reinterpret_cast<bf16x8*>(dst + 8)  = b;
-        *reinterpret_cast<bf16x8*>(dst + 16) = c;
-        *reinterpret_cast<bf16x8*>(dst + 24) = d;
+// Registers of the next tile's V staging: per unit, 8 E4M3 bytes (d0..d0+7)
+// of two consecutive keys and their v_scale; plus one k_scale.
+template <int kReps>
+struct VRaw {
+    u32x2 a[kReps], b[kReps];
+    float sa[kReps], sb[kReps];
+    float ks;
+};
+
+// V staging units: unit u = (key pair kp = u & 31, d group u >> 5 of 8 d).
+template <int kThreads, bool kPaged>
+__device__ __forceinline__ void v_tile_load(VRaw<4096 / 8 / kThreads>& r,
+                                            const uint8_t* __restrict__ v,
+                                            const float* __restrict__ ks,
+                                            const float* __restrict__ vs,
+                                            const TileRows<kPaged>& rows, int kvh, int hkv,
+                                            int tid) {
+    constexpr int kReps = 4096 / 8 / kThreads;
+#pragma unroll
+    for (int rep = 0; rep < kReps; ++rep) {
+        const int     u  = tid + rep * kThreads;
+        const int     kp = u & 31;
+        const int     d0 = 8 * (u >> 5);
+        const int64_t r0 = static_cast<int64_t>(rows(2 * kp)) * hkv + kvh;
+        const int64_t r1 = static_cast<int64_t>(rows(2 * kp + 1)) * hkv + kvh;
+        r.a[rep]  = *reinterpret_cast<const u32x2*>(v + r0 * kHD + d0);
+        r.b[rep]  = *reinterpret_cast<const u32x2*>(v + r1 * kHD + d0);
+        r.sa[rep] = vs[r0];
+        r.sb[rep] = vs[r1];
     }
-    {
-        // Lanes 16i..16i+15 share d0 and cover the 16 key quads, so each
-        // 16-lane pass of the 8-byte LDS writes fills one whole V^T row
-        // (bank-conflict free).
-        const int kq = tid & 15;
-        const int d0 = 8 * (tid >> 4);
-        // 4 keys x 8 bytes -> 8 dwords, each holding one d for the 4 keys.
-        uint32_t x[8];
+    r.ks = ks[static_cast<int64_t>(rows(tid & (kBN - 1))) * hkv + kvh];
+}
+
+// Exponent field of x alone: 2^floor(log2 x) for normal x > 0, 0 for 0.
+__device__ __forceinline__ uint32_t pow2_bits(float x) {
+    return __float_as_uint(x) & 0x7f800000u;
+}
+
+// Writes V'^T = f16(code * v_scale) for the staged units and the k_scale
+// factors of the tile. The two keys of a unit share the larger power of two
+// 2^e of their scales, applied exactly by the converter; the f16 factors
+// v_scale / 2^e (rounded once per key, a relative error below 2^-11 that
+// enters O linearly) are applied with one packed f16 multiply.
+template <int kThreads>
+__device__ __forceinline__ void v_tile_stage(const VRaw<4096 / 8 / kThreads>& r, uint16_t* vt,
+                                             float* kf, int tid, float scale_log2) {
+    constexpr int kReps = 4096 / 8 / kThreads;
+#pragma unroll
+    for (int rep = 0; rep < kReps; ++rep) {
+        const int      u   = tid + rep * kThreads;
+        const int      kp  = u & 31;
+        const int      d0  = 8 * (u >> 5);
+        const uint32_t e   = max(pow2_bits(r.sa[rep]), pow2_bits(r.sb[rep]));
+        const float    p   = __uint_as_float(e);
+        const float    inv = __uint_as_float(0x7f000000u - e);   // 2^-e
+        const f16x2    m   = {static_cast<_Float16>(r.sa[rep] * inv),
+                              static_cast<_Float16>(r.sb[rep] * inv)};
+        uint32_t*      col = reinterpret_cast<uint32_t*>(vt + vt_pos(2 * kp));
 #pragma unroll
         for (int half = 0; half < 2; ++half) {
-            const uint32_t a0 = half ? r.v[0].y : r.v[0].x;
-            const uint32_t a1 = half ? r.v[1].y : r.v[1].x;
-            const uint32_t a2 = half ? r.v[2].y : r.v[2].x;
-            const uint32_t a3 = half ? r.v[3].y : r.v[3].x;
-            const uint32_t t01l = __builtin_amdgcn_perm(a1, a0, 0x05010400u);
-            const uint32_t t01h = __builtin_amdgcn_perm(a1, a0, 0x07030602u);
-            const uint32_t t23l = __builtin_amdgcn_perm(a3, a2, 0x05010400u);
-            const uint32_t t23h = __builtin_amdgcn_perm(a3, a2, 0x07030602u);
-            x[4 * half + 0] = __builtin_amdgcn_perm(t23l, t01l, 0x05040100u);
-            x[4 * half + 1] = __builtin_amdgcn_perm(t23l, t01l, 0x07060302u);
-            x[4 * half + 2] = __builtin_amdgcn_perm(t23h, t01h, 0x05040100u);
-            x[4 * half + 3] = __builtin_amdgcn_perm(t23h, t01h, 0x07060302u);
-        }
-        const int col = vt_pos(4 * kq);
-#pragma unroll
-        for (int dd = 0; dd < 8; ++dd) {
-            *reinterpret_cast<u32x2*>(sVt + (d0 + dd) * kVPitch + col) = e4m3x4_to_bf16x4(x[dd]);
+            const uint32_t wa = half ? r.a[rep].y : r.a[rep].x;
+            const uint32_t wb = half ? r.b[rep].y : r.b[rep].x;
+            // [a0 b0 a1 b1] and [a2 b2 a3 b3]: the two keys of one d per word.
+            const uint32_t lo = __builtin_amdgcn_perm(wb, wa, 0x05010400u);
+            const uint32_t hi = __builtin_amdgcn_perm(wb, wa, 0x07030602u);
+            const int      d  = d0 + 4 * half;
+            const f16x2 x0 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(lo, p, false) * m;
+            const f16x2 x1 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(lo, p, true) * m;
+            const f16x2 x2 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(hi, p, false) * m;
+            const f16x2 x3 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(hi, p, true) * m;
+            col[(d + 0) * (kVPitch / 2)] = __builtin_bit_cast(uint32_t, x0);
+            col[(d + 1) * (kVPitch / 2)] = __builtin_bit_cast(uint32_t, x1);
+            col[(d + 2) * (kVPitch / 2)] = __builtin_bit_cast(uint32_t, x2);
+            col[(d + 3) * (kVPitch / 2)] = __builtin_bit_cast(uint32_t, x3);
         }
     }
     if (tid < kBN) {
-        sKf[tid] = r.sc * scale_log2;
-    } else if (tid < 2 * kBN) {
-        sVf[tid - kBN] = r.sc;
+        kf[tid] = r.ks * scale_log2;
     }
 }
 
-template <bool kPaged>
-__global__ __launch_bounds__(kPfThreads, 2) void flash_prefill_kernel(
+// Four fp32 -> four E4M3 bytes (RNE; inputs within range).
+__device__ __forceinline__ uint32_t pack_e4m3x4(float a, float b, float c, float d) {
+    const int lo = __builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false);
+    return static_cast<uint32_t>(__builtin_amdgcn_cvt_pk_fp8_f32(c, d, lo, true));
+}
+
+template <int kWaves, bool kPaged>
+__global__ __launch_bounds__(kWaves * kWave, 2) void flash_prefill_kernel(
     uint16_t* __restrict__ out, const uint16_t* __restrict__ q,
     const uint8_t* __restrict__ k, const uint8_t* __restrict__ v,
     const float* __restrict__ ks, const float* __restrict__ vs, int n_new,
     const int* __restrict__ cache_len, int hq, int hkv, float scale_log2,
     const int* __restrict__ block_table, int block_shift, bool one_round) {
-    __shared__ __attribute__((aligned(16))) uint16_t sK[kBN * kKPitch];
-    __shared__ __attribute__((aligned(16))) uint16_t sVt[kHD * kVPitch];
-    __shared__ __attribute__((aligned(16))) float    sKf[kBN];
-    __shared__ __attribute__((aligned(16))) float    sVf[kBN];
+    constexpr int kThreads = kWaves * kWave;
+    constexpr int kBM      = 32 * kWaves;           // query rows per workgroup
+    constexpr int kReps    = 4096 / 8 / kThreads;   // V staging units per thread
+
+    // Separate arrays per buffer (not one indexed array), so that the
+    // compiler sees the LDS-DMA into one K buffer and the operand reads from
+    // the other as independent and does not wait for the DMA before them.
+    __shared__ __attribute__((aligned(16))) uint8_t  sK0[kKTile];
+    __shared__ __attribute__((aligned(16))) uint8_t  sK1[kKTile];
+    __shared__ __attribute__((aligned(16))) uint16_t sVt0[kHD * kVPitch];
+    __shared__ __attribute__((aligned(16))) uint16_t sVt1[kHD * kVPitch];
+    __shared__ __attribute__((aligned(16))) float    sKf0[kBN];
+    __shared__ __attribute__((aligned(16))) float    sKf1[kBN];
 
     const int tid  = static_cast<int>(threadIdx.x);
     const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
@@ -177,10 +223,11 @@ __global__ __launch_bounds__(kPfThreads, 2) void flash_prefill_kernel(
     const int qn   = lane & 31;   // query row of this lane within the wave
     const int h    = lane >> 5;   // k-group
 
-    // Block mapping: heavy row blocks first; q heads of one kv head on one XCD.
-    // When the whole grid is resident at once (one_round), the second half of
-    // the grid runs the light blocks in ascending order, so the two
-    // workgroups sharing a compute unit pair a heavy block with a light one.
+    // Heavy (last) row blocks first; q heads of one kv head on one XCD. When
+    // the whole grid is resident at once (one_round, two workgroups per
+    // compute unit), the second half of the grid runs the light blocks in
+    // ascending order, so the two workgroups sharing a compute unit pair a
+    // heavy block with a light one.
     const int n_blk    = (n_new + kBM - 1) / kBM;
     const int bid      = static_cast<int>(blockIdx.x);
     const int half_wgs = (n_blk / 2) * hq;
@@ -188,33 +235,72 @@ __global__ __launch_bounds__(kPfThreads, 2) void flash_prefill_kernel(
                                                         : n_blk - 1 - bid / hq;
     const int hb    = bid % hq;
     const int qh    = ((hq & 7) == 0) ? ((hb & 7) * (hq >> 3) + (hb >> 3)) : hb;
-    const int G     = hq / hkv;
-    const int kvh   = qh / G;
+    const int kvh   = qh / (hq / hkv);
 
-    const int clen  = *cache_len;
-    const int total = clen + n_new;
-    const int q0    = blk * kBM;
-    const int last  = min(q0 + kBM, n_new) - 1;
+    const int clen    = *cache_len;
+    const int total   = clen + n_new;
+    const int q0      = blk * kBM;
+    const int last    = min(q0 + kBM, n_new) - 1;
     const int n_tiles = min((total + kBN - 1) / kBN, (clen + last) / kBN + 1);
 
-    const int wq0        = q0 + wave * 32;                 // first row of this wave
-    const int wlast      = min(wq0 + 31, n_new - 1);       // may be < wq0 (idle wave)
-    const int w_tiles    = (wlast < wq0) ? 0 : (clen + wlast) / kBN + 1;
-    const int my_q       = wq0 + qn;
-    const int my_pos     = clen + my_q;
+    const int wq0     = q0 + wave * 32;              // first row of this wave
+    const int wlast   = min(wq0 + 31, n_new - 1);    // may be < wq0 (idle wave)
+    const int w_tiles = (wlast < wq0) ? 0 : (clen + wlast) / kBN + 1;
+    const int my_q    = wq0 + qn;
+    const int my_pos  = clen + my_q;
 
-    // Q^T (B operand): lane holds row my_q, d = 8h + 16s .. +8 for s = 0..7.
-    bf16x8 qop[8];
+    // Q^T (B operand) as hi + lo E4M3 parts. Lane (row my_q, group h) holds,
+    // for k-step j, d = 64j + 32h .. +32 (the same d the K operand lanes of
+    // group h hold, so the MFMA pairs matching d).
+    i32x8 qhi[2], qlo[2];
+    int   sc_hi, sc_lo;
     {
         const bool      has = my_q < n_new;
         const uint16_t* qr  = q + (static_cast<int64_t>(has ? my_q : 0) * hq + qh) * kHD;
+        float           x[2][32];
+        float           amax = 0.0f;
 #pragma unroll
-        for (int s = 0; s < 8; ++s) {
-            u32x4 w = *reinterpret_cast<const u32x4*>(qr + 8 * h + 16 * s);
-            if (!has) {
-                w = u32x4{0u, 0u, 0u, 0u};
+        for (int j = 0; j < 2; ++j) {
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                u32x4 w = *reinterpret_cast<const u32x4*>(qr + 64 * j + 32 * h + 8 * c);
+                if (!has) {
+                    w = u32x4{0u, 0u, 0u, 0u};
+                }
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    x[j][8 * c + 2 * i]     = __uint_as_float(w[i] << 16);
+                    x[j][8 * c + 2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+                    amax = fmaxf(amax, fmaxf(fabsf(x[j][8 * c + 2 * i]),
+                                             fabsf(x[j][8 * c + 2 * i + 1])));
+                }
             }
-            qop[s] = __builtin_bit_cast(bf16x8, w);
+        }
+        amax = wave_xor_max(amax, 32);
+        // 2^a with amax * 2^a in [128, 256); a zero row keeps a = 0.
+        const int a = (amax > 0.0f) ? 7 - (static_cast<int>(pow2_bits(amax) >> 23) - 127) : 0;
+        const float s2a = __uint_as_float(static_cast<uint32_t>(127 + a) << 23);
+        sc_hi = min(max(kE8M0One - a, 0), 254);
+        sc_lo = min(max(kE8M0One - a - 4, 0), 254);
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+#pragma unroll
+            for (int w = 0; w < 8; ++w) {
+                float y[4], r[4];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    y[i] = x[j][4 * w + i] * s2a;
+                }
+                const uint32_t hw = pack_e4m3x4(y[0], y[1], y[2], y[3]);
+                const f32x2    h0 = __builtin_amdgcn_cvt_pk_f32_fp8(static_cast<int>(hw), false);
+                const f32x2    h1 = __builtin_amdgcn_cvt_pk_f32_fp8(static_cast<int>(hw), true);
+                r[0] = (y[0] - h0.x) * 16.0f;
+                r[1] = (y[1] - h0.y) * 16.0f;
+                r[2] = (y[2] - h1.x) * 16.0f;
+                r[3] = (y[3] - h1.y) * 16.0f;
+                qhi[j][w] = static_cast<int>(hw);
+                qlo[j][w] = static_cast<int>(pack_e4m3x4(r[0], r[1], r[2], r[3]));
+            }
         }
     }
 
@@ -226,166 +312,165 @@ __global__ __launch_bounds__(kPfThreads, 2) void flash_prefill_kernel(
     float m_ref = 0.0f;   // lazy reference maximum of this lane's row (log2 units)
     float l_run = 0.0f;
 
-    PfRaw raw;
-    pf_load<kPaged>(raw, k, v, ks, vs, 0, total, kvh, hkv, tid, block_table, block_shift);
+    // Prologue: tile 0 into buffer 0, tile 1's loads in flight.
+    VRaw<kReps> raw;
+    {
+        const TileRows<kPaged> r0(0, total, block_table, block_shift);
+        k_tile_dma<kThreads>(sK0, k, r0, kvh, hkv, tid);
+        v_tile_load<kThreads>(raw, v, ks, vs, r0, kvh, hkv, tid);
+        v_tile_stage<kThreads>(raw, sVt0, sKf0, tid, scale_log2);
+    }
+    __syncthreads();
 
-    for (int kt = 0; kt < n_tiles; ++kt) {
-        __syncthreads();
-        pf_stage(raw, sK, sVt, sKf, sVf, tid, scale_log2);
-        __syncthreads();
-        if (kt + 1 < n_tiles) {
-            pf_load<kPaged>(raw, k, v, ks, vs, (kt + 1) * kBN, total, kvh, hkv, tid, block_table,
-                            block_shift);
+    // One tile from buffer B (static, so each buffer is a distinct array).
+    auto tile = [&]<int B>(int kt) {
+        uint8_t*  kt_s = B ? sK1 : sK0;
+        uint16_t* vt   = B ? sVt1 : sVt0;
+        float*    kf   = B ? sKf1 : sKf0;
+        uint8_t*  nk   = B ? sK0 : sK1;
+        uint16_t* nvt  = B ? sVt0 : sVt1;
+        float*    nkf  = B ? sKf0 : sKf1;
+        const bool more = kt + 1 < n_tiles;
+        if (more) {
+            const TileRows<kPaged> rn((kt + 1) * kBN, total, block_table, block_shift);
+            k_tile_dma<kThreads>(nk, k, rn, kvh, hkv, tid);
+            v_tile_load<kThreads>(raw, v, ks, vs, rn, kvh, hkv, tid);
         }
-        if (kt >= w_tiles) {
-            continue;
-        }
-        const int key0 = kt * kBN;
+        if (kt < w_tiles) {
+            const int key0 = kt * kBN;
 
-        // S^T = K Q^T for two 32-key blocks. The LDS operand reads run four
-        // MFMAs ahead (scheduling groups), so their latency is hidden.
-        f32x16 s[2];
-        {
-            bf16x8 ka[2][8];
-#pragma unroll
-            for (int kb = 0; kb < 2; ++kb) {
-                const uint16_t* arow = sK + (32 * kb + qn) * kKPitch + 8 * h;
-#pragma unroll
-                for (int st = 0; st < 8; ++st) {
-                    ka[kb][st] = *reinterpret_cast<const bf16x8*>(arow + 16 * st);
-                }
-            }
+            // S^T = K Q^T: per 32-key block, two k-steps of 64 d, each as
+            // hi and lo MFMAs sharing the K operand.
+            f32x16 s[2];
 #pragma unroll
             for (int kb = 0; kb < 2; ++kb) {
                 s[kb] = f32x16{};
+                const int r = 32 * kb + qn;
 #pragma unroll
-                for (int st = 0; st < 8; ++st) {
-                    s[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ka[kb][st], qop[st], s[kb], 0, 0, 0);
+                for (int j = 0; j < 2; ++j) {
+                    const int c0 = 4 * j + 2 * h;
+                    const u32x4 lo = *reinterpret_cast<const u32x4*>(kt_s + k_chunk(r, c0));
+                    const u32x4 hi = *reinterpret_cast<const u32x4*>(kt_s + k_chunk(r, c0 + 1));
+                    const i32x8 ka = {static_cast<int>(lo.x), static_cast<int>(lo.y),
+                                      static_cast<int>(lo.z), static_cast<int>(lo.w),
+                                      static_cast<int>(hi.x), static_cast<int>(hi.y),
+                                      static_cast<int>(hi.z), static_cast<int>(hi.w)};
+                    s[kb] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
+                        ka, qhi[j], s[kb], 0, 0, 0, kE8M0One, 0, sc_hi);
+                    s[kb] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
+                        ka, qlo[j], s[kb], 0, 0, 0, kE8M0One, 0, sc_lo);
                 }
             }
-            __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
-#pragma unroll
-            for (int i = 0; i < 12; ++i) {
-                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-            }
-            __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
-        }
 
-        // t = s * (k_scale * scale * log2 e) - m_ref, one fma per score, in
-        // place. Register r of block kb is key 32kb + 8(r/4) + 4h + r%4 of the
-        // tile.
-#pragma unroll
-        for (int kb = 0; kb < 2; ++kb) {
-#pragma unroll
-            for (int rg = 0; rg < 4; ++rg) {
-                const f32x4 kf = *reinterpret_cast<const f32x4*>(sKf + 32 * kb + 8 * rg + 4 * h);
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    s[kb][4 * rg + e] = fmaf(s[kb][4 * rg + e], kf[e], -m_ref);
-                }
-            }
-        }
-        // Causal / key-end mask, only on tiles that cross the diagonal or the
-        // end of the keys (a wave-uniform branch).
-        if ((key0 + kBN - 1 > clen + wq0) || (key0 + kBN > total)) {
+            // t = s * (k_scale * scale * log2 e) - m_ref, one fma per score.
+            // Register r of block kb is key 32kb + 8(r/4) + 4h + r%4 of the tile.
 #pragma unroll
             for (int kb = 0; kb < 2; ++kb) {
 #pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    const int kp = key0 + 32 * kb + 8 * (r >> 2) + 4 * h + (r & 3);
-                    if (kp > my_pos || kp >= total) {
-                        s[kb][r] = -INFINITY;
+                for (int rg = 0; rg < 4; ++rg) {
+                    const f32x4 f = *reinterpret_cast<const f32x4*>(kf + 32 * kb + 8 * rg + 4 * h);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        s[kb][4 * rg + e] = fmaf(s[kb][4 * rg + e], f[e], -m_ref);
                     }
                 }
             }
-        }
-
-        // p = 2^t against the lazy reference maximum m_ref, the row sum of p
-        // and the P^T operands (p * v_scale rounded to bf16).
-        bf16x8 pop[4];
-        float  psum  = 0.0f;
-        auto   exp_p = [&]() {
-            psum = 0.0f;
+            // Causal / key-end mask, only on tiles that cross the diagonal or
+            // the end of the keys (a wave-uniform branch).
+            if ((key0 + kBN - 1 > clen + wq0) || (key0 + kBN > total)) {
 #pragma unroll
-            for (int kb = 0; kb < 2; ++kb) {
+                for (int kb = 0; kb < 2; ++kb) {
 #pragma unroll
-                for (int half = 0; half < 2; ++half) {
-                    u32x4 pw;
-#pragma unroll
-                    for (int rr = 0; rr < 2; ++rr) {
-                        const int   rg = 2 * half + rr;
-                        const f32x4 vf = *reinterpret_cast<const f32x4*>(sVf + 32 * kb + 8 * rg + 4 * h);
-                        const float p0 = __builtin_amdgcn_exp2f(s[kb][4 * rg + 0]);
-                        const float p1 = __builtin_amdgcn_exp2f(s[kb][4 * rg + 1]);
-                        const float p2 = __builtin_amdgcn_exp2f(s[kb][4 * rg + 2]);
-                        const float p3 = __builtin_amdgcn_exp2f(s[kb][4 * rg + 3]);
-                        psum += (p0 + p1) + (p2 + p3);
-                        pw[2 * rr]     = pack_bf16x2(p0 * vf[0], p1 * vf[1]);
-                        pw[2 * rr + 1] = pack_bf16x2(p2 * vf[2], p3 * vf[3]);
+                    for (int r = 0; r < 16; ++r) {
+                        const int kp = key0 + 32 * kb + 8 * (r >> 2) + 4 * h + (r & 3);
+                        if (kp > my_pos || kp >= total) {
+                            s[kb][r] = -INFINITY;
+                        }
                     }
-                    pop[2 * kb + half] = __builtin_bit_cast(bf16x8, pw);
                 }
             }
-        };
-        exp_p();
-        // Lazy reference maximum (exact): m_ref moves to the row maximum only
-        // on the first tile or when a row sum exceeds 2^64 (some score more
-        // than 64 above m_ref); otherwise the tile needs no max reduction, no
-        // cross-lane step and no accumulator rescale. Every p and l use the
-        // same m_ref, and p <= 2^64 keeps l and O finite in fp32.
-        if (__any((kt == 0) || !(psum <= 0x1p64f))) {
-            float tmax = -INFINITY;
+
+            // p = 2^t rounded to f16 (the P^T operands), and the row sum of
+            // those f16 values.
+            f16x8 pop[4];
+            float psum  = 0.0f;
+            auto  exp_p = [&]() {
+                float part[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-            for (int kb = 0; kb < 2; ++kb) {
+                for (int kb = 0; kb < 2; ++kb) {
 #pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    tmax = fmaxf(tmax, s[kb][r]);
+                    for (int half = 0; half < 2; ++half) {
+                        f16x8 pw;
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) {
+                            const int   r  = 8 * half + 2 * i;
+                            const f16x2 pp = {
+                                static_cast<_Float16>(__builtin_amdgcn_exp2f(s[kb][r])),
+                                static_cast<_Float16>(__builtin_amdgcn_exp2f(s[kb][r + 1]))};
+                            part[i] = __builtin_amdgcn_fdot2(pp, f16x2{1.0f16, 1.0f16}, part[i], false);
+                            pw[2 * i]     = pp.x;
+                            pw[2 * i + 1] = pp.y;
+                        }
+                        pop[2 * kb + half] = pw;
+                    }
                 }
-            }
-            tmax              = wave_xor_max(tmax, 32);
-            const float delta = (tmax == -INFINITY) ? 0.0f : tmax;
-            // On the first tile l and O are still zero (and 2^-delta may be inf).
-            const float alpha = (kt == 0) ? 1.0f : __builtin_amdgcn_exp2f(-delta);
-#pragma unroll
-            for (int kb = 0; kb < 2; ++kb) {
-                s[kb] -= delta;
-            }
-            m_ref += delta;
-            l_run *= alpha;
-#pragma unroll
-            for (int db = 0; db < 4; ++db) {
-                o[db] *= alpha;
-            }
+                psum = (part[0] + part[1]) + (part[2] + part[3]);
+            };
             exp_p();
-        }
-        l_run += psum;
+            // Lazy reference maximum (exact): m_ref moves to the row maximum
+            // only on a wave's first tile or when a row sum exceeds 2^15 (some
+            // score more than 15 above m_ref); otherwise the tile needs no max
+            // reduction, no cross-lane step and no accumulator rescale. Every
+            // p and l use the same m_ref, and p <= 2^15 keeps every p inside
+            // the f16 range.
+            if (__any((kt == 0) || !(psum <= 0x1p15f))) {
+                float tmax = -INFINITY;
+#pragma unroll
+                for (int kb = 0; kb < 2; ++kb) {
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) {
+                        tmax = fmaxf(tmax, s[kb][r]);
+                    }
+                }
+                tmax              = wave_xor_max(tmax, 32);
+                const float delta = (tmax == -INFINITY) ? 0.0f : tmax;
+                // On the first tile l and O are still zero (and 2^-delta may be inf).
+                const float alpha = (kt == 0) ? 1.0f : __builtin_amdgcn_exp2f(-delta);
+#pragma unroll
+                for (int kb = 0; kb < 2; ++kb) {
+                    s[kb] -= delta;
+                }
+                m_ref += delta;
+                l_run *= alpha;
+#pragma unroll
+                for (int db = 0; db < 4; ++db) {
+                    o[db] *= alpha;
+                }
+                exp_p();
+            }
+            l_run += psum;
 
-        // O^T += V^T P^T, operand reads four MFMAs ahead as above.
-        {
-            bf16x8 va[4][4];
+            // O^T += V^T P^T.
 #pragma unroll
             for (int db = 0; db < 4; ++db) {
-                const uint16_t* arow = sVt + (32 * db + qn) * kVPitch + 8 * h;
+                const uint16_t* arow = vt + (32 * db + qn) * kVPitch + 8 * h;
 #pragma unroll
                 for (int t = 0; t < 4; ++t) {
-                    va[db][t] = *reinterpret_cast<const bf16x8*>(arow + 16 * t);
+                    const f16x8 va = *reinterpret_cast<const f16x8*>(arow + 16 * t);
+                    o[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, pop[t], o[db], 0, 0, 0);
                 }
             }
-#pragma unroll
-            for (int db = 0; db < 4; ++db) {
-#pragma unroll
-                for (int t = 0; t < 4; ++t) {
-                    o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va[db][t], pop[t], o[db], 0, 0, 0);
-                }
-            }
-            __builtin_amdgcn_sched_group_barrier(0x100, 4, 1);
-#pragma unroll
-            for (int i = 0; i < 12; ++i) {
-                __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);
-                __builtin_amdgcn_sched_group_barrier(0x100, 1, 1);
-            }
-            __builtin_amdgcn_sched_group_barrier(0x008, 4, 1);
+        }
+        if (more) {
+            v_tile_stage<kThreads>(raw, nvt, nkf, tid, scale_log2);
+        }
+        __syncthreads();
+    };
+
+    for (int kt = 0; kt < n_tiles; kt += 2) {
+        tile.template operator()<0>(kt);
+        if (kt + 1 < n_tiles) {
+            tile.template operator()<1>(kt + 1);
         }
     }
 
@@ -406,6 +491,24 @@ __global__ __launch_bounds__(kPfThreads, 2) void flash_prefill_kernel(
     }
 }
 
+template <int kWaves>
+void launch_prefill(uint16_t* out, const uint16_t* q, const uint8_t* k, const uint8_t* v,
+                    const float* k_scale, const float* v_scale, int n_new, const int* cache_len,
+                    int hq, int hkv, float scale_log2, hipStream_t stream,
+                    const int* block_table, int block_shift, bool one_round) {
+    const int  n_blk = (n_new + 32 * kWaves - 1) / (32 * kWaves);
+    const dim3 grid(static_cast<unsigned>(n_blk * hq));
+    if (block_table != nullptr) {
+        hipLaunchKernelGGL((flash_prefill_kernel<kWaves, true>), grid, dim3(kWaves * kWave), 0,
+                           stream, out, q, k, v, k_scale, v_scale, n_new, cache_len, hq, hkv,
+                           scale_log2, block_table, block_shift, one_round);
+    } else {
+        hipLaunchKernelGGL((flash_prefill_kernel<kWaves, false>), grid, dim3(kWaves * kWave), 0,
+                           stream, out, q, k, v, k_scale, v_scale, n_new, cache_len, hq, hkv,
+                           scale_log2, nullptr, 0, one_round);
+    }
+}
+
 }  // namespace
 
 hipError_t flash_prefill_launch(uint16_t* out, const uint16_t* q,
@@ -418,23 +521,23 @@ hipError_t flash_prefill_launch(uint16_t* out, const uint16_t* q,
     if (head_dim != kHD) {
         return hipErrorInvalidValue;
     }
-    const int  n_blk = (n_new + kBM - 1) / kBM;
-    const dim3 grid(static_cast<unsigned>(n_blk * num_q_heads));
-    // Two workgroups fit per compute unit (LDS and registers).
+    // 8-wave workgroups (256 rows, one per compute unit: half the staging
+    // per wave) when the grid takes at least two rounds of them; otherwise
+    // 4-wave workgroups (128 rows, two per compute unit) with heavy/light
+    // pairing, which balance the causal work of a single round better.
     int dev = 0, cus = 0;
     if (hipGetDevice(&dev) != hipSuccess ||
         hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) {
         cus = 0;
     }
-    const bool one_round = n_blk * num_q_heads <= 2 * cus;
-    if (block_table != nullptr) {
-        hipLaunchKernelGGL(flash_prefill_kernel<true>, grid, dim3(kPfThreads), 0, stream, out, q,
-                           k, v, k_scale, v_scale, n_new, cache_len, num_q_heads, num_kv_heads,
-                           scale * kLog2e, block_table, block_shift, one_round);
+    const float sl = scale * kLog2e;
+    if (((n_new + 255) / 256) * num_q_heads >= 2 * cus) {
+        launch_prefill<8>(out, q, k, v, k_scale, v_scale, n_new, cache_len, num_q_heads,
+                          num_kv_heads, sl, stream, block_table, block_shift, false);
     } else {
-        hipLaunchKernelGGL(flash_prefill_kernel<false>, grid, dim3(kPfThreads), 0, stream, out,
-                           q, k, v, k_scale, v_scale, n_new, cache_len, num_q_heads,
-                           num_kv_heads, scale * kLog2e, nullptr, 0, one_round);
+        const bool one_round = ((n_new + 127) / 128) * num_q_heads <= 2 * cus;
+        launch_prefill<4>(out, q, k, v, k_scale, v_scale, n_new, cache_len, num_q_heads,
+                          num_kv_heads, sl, stream, block_table, block_shift, one_round);
     }
     return hipGetLastError();
 }
