@@ -68,14 +68,15 @@ __device__ __forceinline__ int pf_row(int key, const int* __restrict__ block_tab
 }
 
 // Physical row of key `key` of the tile starting at key0, clamped to the last
-// key. Paged: the tile's two 32-key halves each lie inside one block (blocks
-// hold a power of two >= 32 keys), so two uniform lookups per tile suffice.
+// key (a tile past the end maps to the last tile). Paged: the tile's two
+// 32-key halves each lie inside one block (blocks hold a power of two >= 32
+// keys), so two uniform lookups per tile suffice.
 template <bool kPaged>
 struct TileRows {
     int key0, total, d_lo, d_hi;
     __device__ __forceinline__ TileRows(int key0_, int total_, const int* __restrict__ bt,
                                         int bshift)
-        : key0(key0_), total(total_), d_lo(0), d_hi(0) {
+        : key0(min(key0_, (total_ - 1) & ~(kBN - 1))), total(total_), d_lo(0), d_hi(0) {
         if constexpr (kPaged) {
             d_lo = pf_row<true>(key0, bt, bshift) - key0;
             d_hi = (key0 + 32 < total) ? pf_row<true>(key0 + 32, bt, bshift) - (key0 + 32) : d_lo;
@@ -330,14 +331,16 @@ __global__ __launch_bounds__(kWaves * kWave, 2) void flash_prefill_kernel(
         uint8_t*  nk   = B ? sK0 : sK1;
         uint16_t* nvt  = B ? sVt0 : sVt1;
         float*    nkf  = B ? sKf0 : sKf1;
-        const bool more = kt + 1 < n_tiles;
-        if (more) {
-            const TileRows<kPaged> rn((kt + 1) * kBN, total, block_table, block_shift);
-            k_tile_dma<kThreads>(nk, k, rn, kvh, hkv, tid);
-            v_tile_load<kThreads>(raw, v, ks, vs, rn, kvh, hkv, tid);
-        }
+        // Tile kt + 1 is copied and loaded at the top and staged at the end
+        // of every tile; after the last tile this repeats the last tile into
+        // the idle buffers, which nobody reads. Doing it unconditionally
+        // keeps the copies and the staging in the same scheduling regions
+        // as the MFMAs, whose execution hides their VALU work.
+        const TileRows<kPaged> rn((kt + 1) * kBN, total, block_table, block_shift);
         if (kt < w_tiles) {
             const int key0 = kt * kBN;
+            k_tile_dma<kThreads>(nk, k, rn, kvh, hkv, tid);
+            v_tile_load<kThreads>(raw, v, ks, vs, rn, kvh, hkv, tid);
 
             // S^T = K Q^T: per 32-key block, two k-steps of 64 d, each as
             // hi and lo MFMAs sharing the K operand.
@@ -360,6 +363,13 @@ __global__ __launch_bounds__(kWaves * kWave, 2) void flash_prefill_kernel(
                     s[kb] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
                         ka, qlo[j], s[kb], 0, 0, 0, kE8M0One, 0, sc_lo);
                 }
+            }
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
+                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);   // LDS read
+                __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);   // VALU
+                __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);   // global load
             }
 
             // t = s * (k_scale * scale * log2 e) - m_ref, one fma per score.
@@ -460,8 +470,17 @@ __global__ __launch_bounds__(kWaves * kWave, 2) void flash_prefill_kernel(
                     o[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, pop[t], o[db], 0, 0, 0);
                 }
             }
-        }
-        if (more) {
+            v_tile_stage<kThreads>(raw, nvt, nkf, tid, scale_log2);
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);   // MFMA
+                __builtin_amdgcn_sched_group_barrier(0x100, 1, 1);   // LDS read
+                __builtin_amdgcn_sched_group_barrier(0x002, 2, 1);   // VALU
+                __builtin_amdgcn_sched_group_barrier(0x200, 1, 1);   // LDS write
+            }
+        } else {
+            k_tile_dma<kThreads>(nk, k, rn, kvh, hkv, tid);
+            v_tile_load<kThreads>(raw, v, ks, vs, rn, kvh, hkv, tid);
             v_tile_stage<kThreads>(raw, nvt, nkf, tid, scale_log2);
         }
         __syncthreads();
