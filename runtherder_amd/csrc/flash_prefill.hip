@@ -197,6 +197,21 @@ __device__ __forceinline__ uint32_t pack_e4m3x4(float a, float b, float c, float
     return static_cast<uint32_t>(__builtin_amdgcn_cvt_pk_fp8_f32(c, d, lo, true));
 }
 
+// Workgroup barrier that orders LDS accesses only: waits for this wave's LDS
+// operations, not for its outstanding global loads.
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// s_waitcnt immediate (gfx9 encoding: vmcnt in bits 3:0 and 15:14, expcnt
+// 6:4, lgkmcnt 11:8) waiting until at most n vector-memory operations are
+// outstanding, and for nothing else.
+constexpr int waitcnt_vm(int n) {
+    return (n & 0xf) | (0x7 << 4) | (0xf << 8) | ((n >> 4) << 14);
+}
+
 template <int kWaves, bool kPaged>
 __global__ __launch_bounds__(kWaves * kWave, 2) void flash_prefill_kernel(
     uint16_t* __restrict__ out, const uint16_t* __restrict__ q,
@@ -207,6 +222,8 @@ __global__ __launch_bounds__(kWaves * kWave, 2) void flash_prefill_kernel(
     constexpr int kThreads = kWaves * kWave;
     constexpr int kBM      = 32 * kWaves;           // query rows per workgroup
     constexpr int kReps    = 4096 / 8 / kThreads;   // V staging units per thread
+    // Vector-memory operations of one v_tile_load (4 per unit, 1 k_scale).
+    constexpr int kWaitAllButVLoads = waitcnt_vm(4 * kReps + 1);
 
     // Separate arrays per buffer (not one indexed array), so that the
     // compiler sees the LDS-DMA into one K buffer and the operand reads from
@@ -313,13 +330,19 @@ __global__ __launch_bounds__(kWaves * kWave, 2) void flash_prefill_kernel(
     float m_ref = 0.0f;   // lazy reference maximum of this lane's row (log2 units)
     float l_run = 0.0f;
 
-    // Prologue: tile 0 into buffer 0, tile 1's loads in flight.
-    VRaw<kReps> raw;
+    // V staging registers, two sets: raw0 holds the even tiles, raw1 the odd
+    // ones, so the loads of tile kt + 2 go out a whole tile before the
+    // staging of tile kt + 1 needs its registers.
+    // Prologue: tile 0 staged, K(1) copied, V(1) in raw1.
+    VRaw<kReps> raw0, raw1;
     {
         const TileRows<kPaged> r0(0, total, block_table, block_shift);
+        const TileRows<kPaged> r1(kBN, total, block_table, block_shift);
         k_tile_dma<kThreads>(sK0, k, r0, kvh, hkv, tid);
-        v_tile_load<kThreads>(raw, v, ks, vs, r0, kvh, hkv, tid);
-        v_tile_stage<kThreads>(raw, sVt0, sKf0, tid, scale_log2);
+        v_tile_load<kThreads>(raw0, v, ks, vs, r0, kvh, hkv, tid);
+        v_tile_stage<kThreads>(raw0, sVt0, sKf0, tid, scale_log2);
+        k_tile_dma<kThreads>(sK1, k, r1, kvh, hkv, tid);
+        v_tile_load<kThreads>(raw1, v, ks, vs, r1, kvh, hkv, tid);
     }
     __syncthreads();
 
@@ -331,16 +354,23 @@ __global__ __launch_bounds__(kWaves * kWave, 2) void flash_prefill_kernel(
         uint8_t*  nk   = B ? sK0 : sK1;
         uint16_t* nvt  = B ? sVt0 : sVt1;
         float*    nkf  = B ? sKf0 : sKf1;
-        // Tile kt + 1 is copied and loaded at the top and staged at the end
-        // of every tile; after the last tile this repeats the last tile into
-        // the idle buffers, which nobody reads. Doing it unconditionally
-        // keeps the copies and the staging in the same scheduling regions
-        // as the MFMAs, whose execution hides their VALU work.
-        const TileRows<kPaged> rn((kt + 1) * kBN, total, block_table, block_shift);
+        // On entry V(kt + 1) is in registers rawn (loaded during tile
+        // kt - 1). This tile copies K(kt + 1) into K buffer 1 - B, loads
+        // V(kt + 2) into rawc (issued after the copy, so that waiting for
+        // all but the V loads at the barrier covers the copy) and stages
+        // V(kt + 1) into V^T buffer 1 - B. Past the end the copies repeat
+        // the last tile into idle buffers, which nobody reads; doing them
+        // unconditionally keeps the copies and the staging in the same
+        // scheduling regions as the MFMAs, whose execution hides their VALU
+        // work.
+        VRaw<kReps>& rawc = B ? raw1 : raw0;
+        VRaw<kReps>& rawn = B ? raw0 : raw1;
+        const TileRows<kPaged> r1((kt + 1) * kBN, total, block_table, block_shift);
+        const TileRows<kPaged> r2((kt + 2) * kBN, total, block_table, block_shift);
         if (kt < w_tiles) {
             const int key0 = kt * kBN;
-            k_tile_dma<kThreads>(nk, k, rn, kvh, hkv, tid);
-            v_tile_load<kThreads>(raw, v, ks, vs, rn, kvh, hkv, tid);
+            k_tile_dma<kThreads>(nk, k, r1, kvh, hkv, tid);
+            v_tile_load<kThreads>(rawc, v, ks, vs, r2, kvh, hkv, tid);
 
             // S^T = K Q^T: per 32-key block, two k-steps of 64 d, each as
             // hi and lo MFMAs sharing the K operand.
@@ -470,7 +500,7 @@ __global__ __launch_bounds__(kWaves * kWave, 2) void flash_prefill_kernel(
                     o[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, pop[t], o[db], 0, 0, 0);
                 }
             }
-            v_tile_stage<kThreads>(raw, nvt, nkf, tid, scale_log2);
+            v_tile_stage<kThreads>(rawn, nvt, nkf, tid, scale_log2);
 #pragma unroll
             for (int i = 0; i < 16; ++i) {
                 __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);   // MFMA
@@ -479,11 +509,14 @@ __global__ __launch_bounds__(kWaves * kWave, 2) void flash_prefill_kernel(
                 __builtin_amdgcn_sched_group_barrier(0x200, 1, 1);   // LDS write
             }
         } else {
-            k_tile_dma<kThreads>(nk, k, rn, kvh, hkv, tid);
-            v_tile_load<kThreads>(raw, v, ks, vs, rn, kvh, hkv, tid);
-            v_tile_stage<kThreads>(raw, nvt, nkf, tid, scale_log2);
+            k_tile_dma<kThreads>(nk, k, r1, kvh, hkv, tid);
+            v_tile_load<kThreads>(rawc, v, ks, vs, r2, kvh, hkv, tid);
+            v_tile_stage<kThreads>(rawn, nvt, nkf, tid, scale_log2);
         }
-        __syncthreads();
+        // K(kt + 1) must have landed and the staged LDS writes be visible
+        // before the next tile; the V loads of tile kt + 2 stay in flight.
+        __builtin_amdgcn_s_waitcnt(kWaitAllButVLoads);
+        lds_barrier();
     };
 
     for (int kt = 0; kt < n_tiles; kt += 2) {
