@@ -230,6 +230,8 @@ __global__ __launch_bounds__(kWaves * kWave, 2) void flash_prefill_kernel(
     // the other as independent and does not wait for the DMA before them.
     __shared__ __attribute__((aligned(16))) uint8_t  sK0[kKTile];
     __shared__ __attribute__((aligned(16))) uint8_t  sK1[kKTile];
+    __shared__ __attribute__((aligned(16))) uint8_t  sK2[kKTile];   // 8-wave path only
+    __shared__ __attribute__((aligned(16))) uint8_t  sK3[kKTile];   // 8-wave path only
     __shared__ __attribute__((aligned(16))) uint16_t sVt0[kHD * kVPitch];
     __shared__ __attribute__((aligned(16))) uint16_t sVt1[kHD * kVPitch];
     __shared__ __attribute__((aligned(16))) float    sKf0[kBN];
@@ -330,93 +332,65 @@ __global__ __launch_bounds__(kWaves * kWave, 2) void flash_prefill_kernel(
     float m_ref = 0.0f;   // lazy reference maximum of this lane's row (log2 units)
     float l_run = 0.0f;
 
-    // V staging registers, two sets: raw0 holds the even tiles, raw1 the odd
-    // ones, so the loads of tile kt + 2 go out a whole tile before the
-    // staging of tile kt + 1 needs its registers.
-    // Prologue: tile 0 staged, K(1) copied, V(1) in raw1.
-    VRaw<kReps> raw0, raw1;
-    {
-        const TileRows<kPaged> r0(0, total, block_table, block_shift);
-        const TileRows<kPaged> r1(kBN, total, block_table, block_shift);
-        k_tile_dma<kThreads>(sK0, k, r0, kvh, hkv, tid);
-        v_tile_load<kThreads>(raw0, v, ks, vs, r0, kvh, hkv, tid);
-        v_tile_stage<kThreads>(raw0, sVt0, sKf0, tid, scale_log2);
-        k_tile_dma<kThreads>(sK1, k, r1, kvh, hkv, tid);
-        v_tile_load<kThreads>(raw1, v, ks, vs, r1, kvh, hkv, tid);
-    }
-    __syncthreads();
+    if constexpr (kWaves == 8) {
+        // The two waves sharing a SIMD (w and w + 4) run each tile in
+        // different phase orders so that one's softmax (VALU) meets the
+        // other's MFMAs: the early group (waves 0-3) copies the next K tile
+        // and does scores, softmax, P V of tile kt; the late group (waves
+        // 4-7) does P V of tile kt - 1 (its P kept in registers across the
+        // barrier), scores and softmax of tile kt, then stages V(kt + 1) into
+        // the V^T buffer it has just finished reading.
+        const bool late = wave >= kWaves / 2;
+        const int  gtid = tid & (kThreads / 2 - 1);   // thread index within the group
 
-    // One tile from buffer B (static, so each buffer is a distinct array).
-    auto tile = [&]<int B>(int kt) {
-        uint8_t*  kt_s = B ? sK1 : sK0;
-        uint16_t* vt   = B ? sVt1 : sVt0;
-        float*    kf   = B ? sKf1 : sKf0;
-        uint8_t*  nk   = B ? sK0 : sK1;
-        uint16_t* nvt  = B ? sVt0 : sVt1;
-        float*    nkf  = B ? sKf0 : sKf1;
-        // On entry V(kt + 1) is in registers rawn (loaded during tile
-        // kt - 1). This tile copies K(kt + 1) into K buffer 1 - B, loads
-        // V(kt + 2) into rawc (issued after the copy, so that waiting for
-        // all but the V loads at the barrier covers the copy) and stages
-        // V(kt + 1) into V^T buffer 1 - B. Past the end the copies repeat
-        // the last tile into idle buffers, which nobody reads; doing them
-        // unconditionally keeps the copies and the staging in the same
-        // scheduling regions as the MFMAs, whose execution hides their VALU
-        // work.
-        VRaw<kReps>& rawc = B ? raw1 : raw0;
-        VRaw<kReps>& rawn = B ? raw0 : raw1;
-        const TileRows<kPaged> r1((kt + 1) * kBN, total, block_table, block_shift);
-        const TileRows<kPaged> r2((kt + 2) * kBN, total, block_table, block_shift);
-        if (kt < w_tiles) {
-            const int key0 = kt * kBN;
-            k_tile_dma<kThreads>(nk, k, r1, kvh, hkv, tid);
-            v_tile_load<kThreads>(rawc, v, ks, vs, r2, kvh, hkv, tid);
-
-            // S^T = K Q^T: per 32-key block, two k-steps of 64 d, each as
-            // hi and lo MFMAs sharing the K operand.
-            f32x16 s[2];
+        // S^T = K Q^T for one tile (see above); all eight K operand reads
+        // are issued before the first MFMA.
+        auto qk = [&](const uint8_t* kbuf, f32x16 (&sc)[2]) {
+            i32x8 ka[2][2];
 #pragma unroll
             for (int kb = 0; kb < 2; ++kb) {
-                s[kb] = f32x16{};
                 const int r = 32 * kb + qn;
 #pragma unroll
                 for (int j = 0; j < 2; ++j) {
-                    const int c0 = 4 * j + 2 * h;
-                    const u32x4 lo = *reinterpret_cast<const u32x4*>(kt_s + k_chunk(r, c0));
-                    const u32x4 hi = *reinterpret_cast<const u32x4*>(kt_s + k_chunk(r, c0 + 1));
-                    const i32x8 ka = {static_cast<int>(lo.x), static_cast<int>(lo.y),
+                    const int   c0 = 4 * j + 2 * h;
+                    const u32x4 lo = *reinterpret_cast<const u32x4*>(kbuf + k_chunk(r, c0));
+                    const u32x4 hi = *reinterpret_cast<const u32x4*>(kbuf + k_chunk(r, c0 + 1));
+                    ka[kb][j] = i32x8{static_cast<int>(lo.x), static_cast<int>(lo.y),
                                       static_cast<int>(lo.z), static_cast<int>(lo.w),
                                       static_cast<int>(hi.x), static_cast<int>(hi.y),
                                       static_cast<int>(hi.z), static_cast<int>(hi.w)};
-                    s[kb] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
-                        ka, qhi[j], s[kb], 0, 0, 0, kE8M0One, 0, sc_hi);
-                    s[kb] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
-                        ka, qlo[j], s[kb], 0, 0, 0, kE8M0One, 0, sc_lo);
                 }
             }
+            sc[0] = f32x16{};
+            sc[1] = f32x16{};
 #pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
-                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);   // LDS read
-                __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);   // VALU
-                __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);   // global load
+            for (int j = 0; j < 2; ++j) {
+#pragma unroll
+                for (int kb = 0; kb < 2; ++kb) {
+                    sc[kb] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
+                        ka[kb][j], qhi[j], sc[kb], 0, 0, 0, kE8M0One, 0, sc_hi);
+                }
+#pragma unroll
+                for (int kb = 0; kb < 2; ++kb) {
+                    sc[kb] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
+                        ka[kb][j], qlo[j], sc[kb], 0, 0, 0, kE8M0One, 0, sc_lo);
+                }
             }
-
-            // t = s * (k_scale * scale * log2 e) - m_ref, one fma per score.
-            // Register r of block kb is key 32kb + 8(r/4) + 4h + r%4 of the tile.
+        };
+        // Softmax of tile kt's scores into the P^T operands (see above).
+        auto softmax = [&](f32x16 (&sx)[2], const float* kfb, int kt, f16x8 (&pop)[4]) {
+            const int key0 = kt * kBN;
 #pragma unroll
             for (int kb = 0; kb < 2; ++kb) {
 #pragma unroll
                 for (int rg = 0; rg < 4; ++rg) {
-                    const f32x4 f = *reinterpret_cast<const f32x4*>(kf + 32 * kb + 8 * rg + 4 * h);
+                    const f32x4 f = *reinterpret_cast<const f32x4*>(kfb + 32 * kb + 8 * rg + 4 * h);
 #pragma unroll
                     for (int e = 0; e < 4; ++e) {
-                        s[kb][4 * rg + e] = fmaf(s[kb][4 * rg + e], f[e], -m_ref);
+                        sx[kb][4 * rg + e] = fmaf(sx[kb][4 * rg + e], f[e], -m_ref);
                     }
                 }
             }
-            // Causal / key-end mask, only on tiles that cross the diagonal or
-            // the end of the keys (a wave-uniform branch).
             if ((key0 + kBN - 1 > clen + wq0) || (key0 + kBN > total)) {
 #pragma unroll
                 for (int kb = 0; kb < 2; ++kb) {
@@ -424,15 +398,11 @@ __global__ __launch_bounds__(kWaves * kWave, 2) void flash_prefill_kernel(
                     for (int r = 0; r < 16; ++r) {
                         const int kp = key0 + 32 * kb + 8 * (r >> 2) + 4 * h + (r & 3);
                         if (kp > my_pos || kp >= total) {
-                            s[kb][r] = -INFINITY;
+                            sx[kb][r] = -INFINITY;
                         }
                     }
                 }
             }
-
-            // p = 2^t rounded to f16 (the P^T operands), and the row sum of
-            // those f16 values.
-            f16x8 pop[4];
             float psum  = 0.0f;
             auto  exp_p = [&]() {
                 float part[4] = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -445,9 +415,10 @@ __global__ __launch_bounds__(kWaves * kWave, 2) void flash_prefill_kernel(
                         for (int i = 0; i < 4; ++i) {
                             const int   r  = 8 * half + 2 * i;
                             const f16x2 pp = {
-                                static_cast<_Float16>(__builtin_amdgcn_exp2f(s[kb][r])),
-                                static_cast<_Float16>(__builtin_amdgcn_exp2f(s[kb][r + 1]))};
-                            part[i] = __builtin_amdgcn_fdot2(pp, f16x2{1.0f16, 1.0f16}, part[i], false);
+                                static_cast<_Float16>(__builtin_amdgcn_exp2f(sx[kb][r])),
+                                static_cast<_Float16>(__builtin_amdgcn_exp2f(sx[kb][r + 1]))};
+                            part[i] = __builtin_amdgcn_fdot2(pp, f16x2{1.0f16, 1.0f16}, part[i],
+                                                             false);
                             pw[2 * i]     = pp.x;
                             pw[2 * i + 1] = pp.y;
                         }
@@ -457,28 +428,21 @@ __global__ __launch_bounds__(kWaves * kWave, 2) void flash_prefill_kernel(
                 psum = (part[0] + part[1]) + (part[2] + part[3]);
             };
             exp_p();
-            // Lazy reference maximum (exact): m_ref moves to the row maximum
-            // only on a wave's first tile or when a row sum exceeds 2^15 (some
-            // score more than 15 above m_ref); otherwise the tile needs no max
-            // reduction, no cross-lane step and no accumulator rescale. Every
-            // p and l use the same m_ref, and p <= 2^15 keeps every p inside
-            // the f16 range.
             if (__any((kt == 0) || !(psum <= 0x1p15f))) {
                 float tmax = -INFINITY;
 #pragma unroll
                 for (int kb = 0; kb < 2; ++kb) {
 #pragma unroll
                     for (int r = 0; r < 16; ++r) {
-                        tmax = fmaxf(tmax, s[kb][r]);
+                        tmax = fmaxf(tmax, sx[kb][r]);
                     }
                 }
                 tmax              = wave_xor_max(tmax, 32);
                 const float delta = (tmax == -INFINITY) ? 0.0f : tmax;
-                // On the first tile l and O are still zero (and 2^-delta may be inf).
                 const float alpha = (kt == 0) ? 1.0f : __builtin_amdgcn_exp2f(-delta);
 #pragma unroll
                 for (int kb = 0; kb < 2; ++kb) {
-                    s[kb] -= delta;
+                    sx[kb] -= delta;
                 }
                 m_ref += delta;
                 l_run *= alpha;
@@ -489,41 +453,313 @@ __global__ __launch_bounds__(kWaves * kWave, 2) void flash_prefill_kernel(
                 exp_p();
             }
             l_run += psum;
-
-            // O^T += V^T P^T.
+        };
+        // O^T += V^T P^T, the operand reads running four MFMAs ahead.
+        auto pv = [&](const uint16_t* vtb, const f16x8 (&pop)[4]) {
 #pragma unroll
             for (int db = 0; db < 4; ++db) {
-                const uint16_t* arow = vt + (32 * db + qn) * kVPitch + 8 * h;
+                const uint16_t* arow = vtb + (32 * db + qn) * kVPitch + 8 * h;
 #pragma unroll
                 for (int t = 0; t < 4; ++t) {
                     const f16x8 va = *reinterpret_cast<const f16x8*>(arow + 16 * t);
                     o[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, pop[t], o[db], 0, 0, 0);
                 }
             }
-            v_tile_stage<kThreads>(rawn, nvt, nkf, tid, scale_log2);
+            __builtin_amdgcn_sched_group_barrier(0x100, 4, 2);
 #pragma unroll
-            for (int i = 0; i < 16; ++i) {
-                __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);   // MFMA
-                __builtin_amdgcn_sched_group_barrier(0x100, 1, 1);   // LDS read
-                __builtin_amdgcn_sched_group_barrier(0x002, 2, 1);   // VALU
-                __builtin_amdgcn_sched_group_barrier(0x200, 1, 1);   // LDS write
+            for (int i = 0; i < 12; ++i) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 2);
+                __builtin_amdgcn_sched_group_barrier(0x100, 1, 2);
+            }
+            __builtin_amdgcn_sched_group_barrier(0x008, 4, 2);
+        };
+
+        constexpr int kGThreads = kThreads / 2;
+        constexpr int kGReps    = 4096 / 8 / kGThreads;
+        // K codes go through a ring of four buffers, copied two tiles ahead.
+        // Prologue: tile 0 staged by everyone, K(1) copied; V(1) into the
+        // late group's registers.
+        VRaw<kGReps> raw0, raw1;
+        {
+            const TileRows<kPaged> r0(0, total, block_table, block_shift);
+            const TileRows<kPaged> r1(kBN, total, block_table, block_shift);
+            k_tile_dma<kThreads>(sK0, k, r0, kvh, hkv, tid);
+            k_tile_dma<kThreads>(sK1, k, r1, kvh, hkv, tid);
+            VRaw<kReps> rz;
+            v_tile_load<kThreads>(rz, v, ks, vs, r0, kvh, hkv, tid);
+            v_tile_stage<kThreads>(rz, sVt0, sKf0, tid, scale_log2);
+            if (late) {
+                const TileRows<kPaged> r1(kBN, total, block_table, block_shift);
+                v_tile_load<kGThreads>(raw1, v, ks, vs, r1, kvh, hkv, gtid);
+            }
+        }
+        __syncthreads();
+
+        auto kbuf4 = [&]<int R>() -> uint8_t* {
+            if constexpr (R == 0) return sK0;
+            else if constexpr (R == 1) return sK1;
+            else if constexpr (R == 2) return sK2;
+            else return sK3;
+        };
+        if (!late) {
+            constexpr int kDmaOps = kKTile / 16 / kGThreads;   // copies issued per tile
+            auto tile = [&]<int R>(int kt) {
+                constexpr int  B    = R & 1;
+                const uint8_t* kcur = kbuf4.template operator()<R>();
+                uint8_t*       nk   = kbuf4.template operator()<(R + 2) & 3>();
+                const float*   kfb  = B ? sKf1 : sKf0;
+                const uint16_t* vtb = B ? sVt1 : sVt0;
+                const TileRows<kPaged> r2((kt + 2) * kBN, total, block_table, block_shift);
+                k_tile_dma<kGThreads>(nk, k, r2, kvh, hkv, gtid);
+                if (kt < w_tiles) {
+                    f32x16 sx[2];
+                    f16x8  pop[4];
+                    qk(kcur, sx);
+                    softmax(sx, kfb, kt, pop);
+                    pv(vtb, pop);
+                }
+                // K(kt + 1), copied during the previous tile, must have landed;
+                // this tile's copy of K(kt + 2) stays in flight.
+                __builtin_amdgcn_s_waitcnt(waitcnt_vm(kDmaOps));
+                lds_barrier();
+            };
+            for (int kt = 0; kt < n_tiles; kt += 4) {
+                tile.template operator()<0>(kt);
+                if (kt + 1 < n_tiles) tile.template operator()<1>(kt + 1);
+                if (kt + 2 < n_tiles) tile.template operator()<2>(kt + 2);
+                if (kt + 3 < n_tiles) tile.template operator()<3>(kt + 3);
             }
         } else {
-            k_tile_dma<kThreads>(nk, k, r1, kvh, hkv, tid);
-            v_tile_load<kThreads>(rawc, v, ks, vs, r2, kvh, hkv, tid);
-            v_tile_stage<kThreads>(rawn, nvt, nkf, tid, scale_log2);
+            f16x8 pop_keep[4];
+            auto  tile = [&]<int R>(int kt) {
+                constexpr int  B     = R & 1;
+                const uint8_t* kcur  = kbuf4.template operator()<R>();
+                const float*   kfb   = B ? sKf1 : sKf0;
+                uint16_t*      vprev = B ? sVt0 : sVt1;   // V^T(kt - 1), then V^T(kt + 1)
+                float*         nkf   = B ? sKf0 : sKf1;
+                VRaw<kGReps>&  rawc  = B ? raw1 : raw0;
+                VRaw<kGReps>&  rawn  = B ? raw0 : raw1;
+                const TileRows<kPaged> r2((kt + 2) * kBN, total, block_table, block_shift);
+                if (kt >= 1 && kt - 1 < w_tiles) {
+                    pv(vprev, pop_keep);
+                }
+                v_tile_load<kGThreads>(rawc, v, ks, vs, r2, kvh, hkv, gtid);
+                if (kt < w_tiles) {
+                    f32x16 sx[2];
+                    qk(kcur, sx);
+                    softmax(sx, kfb, kt, pop_keep);
+                }
+                v_tile_stage<kGThreads>(rawn, vprev, nkf, gtid, scale_log2);
+                lds_barrier();
+            };
+            for (int kt = 0; kt < n_tiles; kt += 4) {
+                tile.template operator()<0>(kt);
+                if (kt + 1 < n_tiles) tile.template operator()<1>(kt + 1);
+                if (kt + 2 < n_tiles) tile.template operator()<2>(kt + 2);
+                if (kt + 3 < n_tiles) tile.template operator()<3>(kt + 3);
+            }
+            // P V of the last tile.
+            if (n_tiles - 1 < w_tiles) {
+                pv(((n_tiles - 1) & 1) ? sVt1 : sVt0, pop_keep);
+            }
         }
-        // K(kt + 1) must have landed and the staged LDS writes be visible
-        // before the next tile; the V loads of tile kt + 2 stay in flight.
-        __builtin_amdgcn_s_waitcnt(kWaitAllButVLoads);
-        lds_barrier();
-    };
-
-    for (int kt = 0; kt < n_tiles; kt += 2) {
-        tile.template operator()<0>(kt);
-        if (kt + 1 < n_tiles) {
-            tile.template operator()<1>(kt + 1);
+    } else {
+    // V staging registers, two sets: raw0 holds the even tiles, raw1 the odd
+        // ones, so the loads of tile kt + 2 go out a whole tile before the
+        // staging of tile kt + 1 needs its registers.
+        // Prologue: tile 0 staged, K(1) copied, V(1) in raw1.
+        VRaw<kReps> raw0, raw1;
+        {
+            const TileRows<kPaged> r0(0, total, block_table, block_shift);
+            const TileRows<kPaged> r1(kBN, total, block_table, block_shift);
+            k_tile_dma<kThreads>(sK0, k, r0, kvh, hkv, tid);
+            v_tile_load<kThreads>(raw0, v, ks, vs, r0, kvh, hkv, tid);
+            v_tile_stage<kThreads>(raw0, sVt0, sKf0, tid, scale_log2);
+            k_tile_dma<kThreads>(sK1, k, r1, kvh, hkv, tid);
+            v_tile_load<kThreads>(raw1, v, ks, vs, r1, kvh, hkv, tid);
         }
+        __syncthreads();
+    
+        // One tile from buffer B (static, so each buffer is a distinct array).
+        auto tile = [&]<int B>(int kt) {
+            uint8_t*  kt_s = B ? sK1 : sK0;
+            uint16_t* vt   = B ? sVt1 : sVt0;
+            float*    kf   = B ? sKf1 : sKf0;
+            uint8_t*  nk   = B ? sK0 : sK1;
+            uint16_t* nvt  = B ? sVt0 : sVt1;
+            float*    nkf  = B ? sKf0 : sKf1;
+            // On entry V(kt + 1) is in registers rawn (loaded during tile
+            // kt - 1). This tile copies K(kt + 1) into K buffer 1 - B, loads
+            // V(kt + 2) into rawc (issued after the copy, so that waiting for
+            // all but the V loads at the barrier covers the copy) and stages
+            // V(kt + 1) into V^T buffer 1 - B. Past the end the copies repeat
+            // the last tile into idle buffers, which nobody reads; doing them
+            // unconditionally keeps the copies and the staging in the same
+            // scheduling regions as the MFMAs, whose execution hides their VALU
+            // work.
+            VRaw<kReps>& rawc = B ? raw1 : raw0;
+            VRaw<kReps>& rawn = B ? raw0 : raw1;
+            const TileRows<kPaged> r1((kt + 1) * kBN, total, block_table, block_shift);
+            const TileRows<kPaged> r2((kt + 2) * kBN, total, block_table, block_shift);
+            if (kt < w_tiles) {
+                const int key0 = kt * kBN;
+                k_tile_dma<kThreads>(nk, k, r1, kvh, hkv, tid);
+                v_tile_load<kThreads>(rawc, v, ks, vs, r2, kvh, hkv, tid);
+    
+                // S^T = K Q^T: per 32-key block, two k-steps of 64 d, each as
+                // hi and lo MFMAs sharing the K operand.
+                f32x16 s[2];
+    #pragma unroll
+                for (int kb = 0; kb < 2; ++kb) {
+                    s[kb] = f32x16{};
+                    const int r = 32 * kb + qn;
+    #pragma unroll
+                    for (int j = 0; j < 2; ++j) {
+                        const int c0 = 4 * j + 2 * h;
+                        const u32x4 lo = *reinterpret_cast<const u32x4*>(kt_s + k_chunk(r, c0));
+                        const u32x4 hi = *reinterpret_cast<const u32x4*>(kt_s + k_chunk(r, c0 + 1));
+                        const i32x8 ka = {static_cast<int>(lo.x), static_cast<int>(lo.y),
+                                          static_cast<int>(lo.z), static_cast<int>(lo.w),
+                                          static_cast<int>(hi.x), static_cast<int>(hi.y),
+                                          static_cast<int>(hi.z), static_cast<int>(hi.w)};
+                        s[kb] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
+                            ka, qhi[j], s[kb], 0, 0, 0, kE8M0One, 0, sc_hi);
+                        s[kb] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
+                            ka, qlo[j], s[kb], 0, 0, 0, kE8M0One, 0, sc_lo);
+                    }
+                }
+    #pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
+                    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);   // LDS read
+                    __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);   // VALU
+                    __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);   // global load
+                }
+    
+                // t = s * (k_scale * scale * log2 e) - m_ref, one fma per score.
+                // Register r of block kb is key 32kb + 8(r/4) + 4h + r%4 of the tile.
+    #pragma unroll
+                for (int kb = 0; kb < 2; ++kb) {
+    #pragma unroll
+                    for (int rg = 0; rg < 4; ++rg) {
+                        const f32x4 f = *reinterpret_cast<const f32x4*>(kf + 32 * kb + 8 * rg + 4 * h);
+    #pragma unroll
+                        for (int e = 0; e < 4; ++e) {
+                            s[kb][4 * rg + e] = fmaf(s[kb][4 * rg + e], f[e], -m_ref);
+                        }
+                    }
+                }
+                // Causal / key-end mask, only on tiles that cross the diagonal or
+                // the end of the keys (a wave-uniform branch).
+                if ((key0 + kBN - 1 > clen + wq0) || (key0 + kBN > total)) {
+    #pragma unroll
+                    for (int kb = 0; kb < 2; ++kb) {
+    #pragma unroll
+                        for (int r = 0; r < 16; ++r) {
+                            const int kp = key0 + 32 * kb + 8 * (r >> 2) + 4 * h + (r & 3);
+                            if (kp > my_pos || kp >= total) {
+                                s[kb][r] = -INFINITY;
+                            }
+                        }
+                    }
+                }
+    
+                // p = 2^t rounded to f16 (the P^T operands), and the row sum of
+                // those f16 values.
+                f16x8 pop[4];
+                float psum  = 0.0f;
+                auto  exp_p = [&]() {
+                    float part[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    #pragma unroll
+                    for (int kb = 0; kb < 2; ++kb) {
+    #pragma unroll
+                        for (int half = 0; half < 2; ++half) {
+                            f16x8 pw;
+    #pragma unroll
+                            for (int i = 0; i < 4; ++i) {
+                                const int   r  = 8 * half + 2 * i;
+                                const f16x2 pp = {
+                                    static_cast<_Float16>(__builtin_amdgcn_exp2f(s[kb][r])),
+                                    static_cast<_Float16>(__builtin_amdgcn_exp2f(s[kb][r + 1]))};
+                                part[i] = __builtin_amdgcn_fdot2(pp, f16x2{1.0f16, 1.0f16}, part[i], false);
+                                pw[2 * i]     = pp.x;
+                                pw[2 * i + 1] = pp.y;
+                            }
+                            pop[2 * kb + half] = pw;
+                        }
+                    }
+                    psum = (part[0] + part[1]) + (part[2] + part[3]);
+                };
+                exp_p();
+                // Lazy reference maximum (exact): m_ref moves to the row maximum
+                // only on a wave's first tile or when a row sum exceeds 2^15 (some
+                // score more than 15 above m_ref); otherwise the tile needs no max
+                // reduction, no cross-lane step and no accumulator rescale. Every
+                // p and l use the same m_ref, and p <= 2^15 keeps every p inside
+                // the f16 range.
+                if (__any((kt == 0) || !(psum <= 0x1p15f))) {
+                    float tmax = -INFINITY;
+    #pragma unroll
+                    for (int kb = 0; kb < 2; ++kb) {
+    #pragma unroll
+                        for (int r = 0; r < 16; ++r) {
+                            tmax = fmaxf(tmax, s[kb][r]);
+                        }
+                    }
+                    tmax              = wave_xor_max(tmax, 32);
+                    const float delta = (tmax == -INFINITY) ? 0.0f : tmax;
+                    // On the first tile l and O are still zero (and 2^-delta may be inf).
+                    const float alpha = (kt == 0) ? 1.0f : __builtin_amdgcn_exp2f(-delta);
+    #pragma unroll
+                    for (int kb = 0; kb < 2; ++kb) {
+                        s[kb] -= delta;
+                    }
+                    m_ref += delta;
+                    l_run *= alpha;
+    #pragma unroll
+                    for (int db = 0; db < 4; ++db) {
+                        o[db] *= alpha;
+                    }
+                    exp_p();
+                }
+                l_run += psum;
+    
+                // O^T += V^T P^T.
+    #pragma unroll
+                for (int db = 0; db < 4; ++db) {
+                    const uint16_t* arow = vt + (32 * db + qn) * kVPitch + 8 * h;
+    #pragma unroll
+                    for (int t = 0; t < 4; ++t) {
+                        const f16x8 va = *reinterpret_cast<const f16x8*>(arow + 16 * t);
+                        o[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, pop[t], o[db], 0, 0, 0);
+                    }
+                }
+                v_tile_stage<kThreads>(rawn, nvt, nkf, tid, scale_log2);
+    #pragma unroll
+                for (int i = 0; i < 16; ++i) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);   // MFMA
+                    __builtin_amdgcn_sched_group_barrier(0x100, 1, 1);   // LDS read
+                    __builtin_amdgcn_sched_group_barrier(0x002, 2, 1);   // VALU
+                    __builtin_amdgcn_sched_group_barrier(0x200, 1, 1);   // LDS write
+                }
+            } else {
+                k_tile_dma<kThreads>(nk, k, r1, kvh, hkv, tid);
+                v_tile_load<kThreads>(rawc, v, ks, vs, r2, kvh, hkv, tid);
+                v_tile_stage<kThreads>(rawn, nvt, nkf, tid, scale_log2);
+            }
+            // K(kt + 1) must have landed and the staged LDS writes be visible
+            // before the next tile; the V loads of tile kt + 2 stay in flight.
+            __builtin_amdgcn_s_waitcnt(kWaitAllButVLoads);
+            lds_barrier();
+        };
+    
+        for (int kt = 0; kt < n_tiles; kt += 2) {
+            tile.template operator()<0>(kt);
+            if (kt + 1 < n_tiles) {
+                tile.template operator()<1>(kt + 1);
+            }
+        }
+    
     }
 
     const float l_tot = wave_xor_sum(l_run, 32);
