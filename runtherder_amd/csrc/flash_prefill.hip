@@ -503,13 +503,16 @@ __global__ __launch_bounds__(kWaves * kWave, 2) void flash_prefill_kernel(
         };
         if (!late) {
             constexpr int kDmaOps = kKTile / 16 / kGThreads;   // copies issued per tile
+            // Rows of the tile two ahead, looked up (paged) one tile before use.
+            TileRows<kPaged> rn(2 * kBN, total, block_table, block_shift);
             auto tile = [&]<int R>(int kt) {
                 constexpr int  B    = R & 1;
                 const uint8_t* kcur = kbuf4.template operator()<R>();
                 uint8_t*       nk   = kbuf4.template operator()<(R + 2) & 3>();
                 const float*   kfb  = B ? sKf1 : sKf0;
                 const uint16_t* vtb = B ? sVt1 : sVt0;
-                const TileRows<kPaged> r2((kt + 2) * kBN, total, block_table, block_shift);
+                const TileRows<kPaged> r2 = rn;
+                rn = TileRows<kPaged>((kt + 3) * kBN, total, block_table, block_shift);
                 k_tile_dma<kGThreads>(nk, k, r2, kvh, hkv, gtid);
                 if (kt < w_tiles) {
                     f32x16 sx[2];
@@ -531,6 +534,7 @@ __global__ __launch_bounds__(kWaves * kWave, 2) void flash_prefill_kernel(
             }
         } else {
             f16x8 pop_keep[4];
+            TileRows<kPaged> rn(2 * kBN, total, block_table, block_shift);
             auto  tile = [&]<int R>(int kt) {
                 constexpr int  B     = R & 1;
                 const uint8_t* kcur  = kbuf4.template operator()<R>();
@@ -539,7 +543,8 @@ __global__ __launch_bounds__(kWaves * kWave, 2) void flash_prefill_kernel(
                 float*         nkf   = B ? sKf0 : sKf1;
                 VRaw<kGReps>&  rawc  = B ? raw1 : raw0;
                 VRaw<kGReps>&  rawn  = B ? raw0 : raw1;
-                const TileRows<kPaged> r2((kt + 2) * kBN, total, block_table, block_shift);
+                const TileRows<kPaged> r2 = rn;
+                rn = TileRows<kPaged>((kt + 3) * kBN, total, block_table, block_shift);
                 if (kt >= 1 && kt - 1 < w_tiles) {
                     pv(vprev, pop_keep);
                 }
@@ -580,6 +585,10 @@ __global__ __launch_bounds__(kWaves * kWave, 2) void flash_prefill_kernel(
         }
         __syncthreads();
     
+        // Rows of the tiles one and two ahead, looked up (paged) a tile
+        // before use.
+        TileRows<kPaged> rn1(kBN, total, block_table, block_shift);
+        TileRows<kPaged> rn2(2 * kBN, total, block_table, block_shift);
         // One tile from buffer B (static, so each buffer is a distinct array).
         auto tile = [&]<int B>(int kt) {
             uint8_t*  kt_s = B ? sK1 : sK0;
@@ -599,8 +608,10 @@ __global__ __launch_bounds__(kWaves * kWave, 2) void flash_prefill_kernel(
             // work.
             VRaw<kReps>& rawc = B ? raw1 : raw0;
             VRaw<kReps>& rawn = B ? raw0 : raw1;
-            const TileRows<kPaged> r1((kt + 1) * kBN, total, block_table, block_shift);
-            const TileRows<kPaged> r2((kt + 2) * kBN, total, block_table, block_shift);
+            const TileRows<kPaged> r1 = rn1;
+            const TileRows<kPaged> r2 = rn2;
+            rn1 = rn2;
+            rn2 = TileRows<kPaged>((kt + 3) * kBN, total, block_table, block_shift);
             if (kt < w_tiles) {
                 const int key0 = kt * kBN;
                 k_tile_dma<kThreads>(nk, k, r1, kvh, hkv, tid);
