@@ -160,6 +160,27 @@ def test_config4_prefill_sampled_rows(n):
     check_rows(bf16_host(out), q, k8, v8, ks, vs, 0, sampled_rows(n, 12, n), hq, hkv, d, scale)
 
 
+@pytest.mark.parametrize("clen", [0, 37, 100, 165])
+def test_large_grid_ragged_tile_counts(clen):
+    """n_new 4100 takes the 8-wave (two-group) path; with these cache lengths
+    the row blocks' tile counts cover every residue mod 4 of the unrolled tile
+    loop and the last tile is partial. Oracle on sampled rows."""
+    hq, hkv, d, n = 32, 8, 128, 4100
+    total = clen + n
+    scale = np.float32(1.0 / np.sqrt(d))
+    q, k, v = rope_qkv(total, hq, hkv, d, 1e6, False, 4100 + clen)
+    cache, view = append_and_check(0, k, v, hkv, d, total)
+    out = torch.empty((n, hq, d), dtype=torch.bfloat16, device=DEV)
+    step(f"ragged prefill n={n} clen={clen}")
+    R.flash_prefill_bf16(out, bf16_dev(q[clen:]), view.k, view.v, view.k_scale, view.v_scale, n,
+                         int_dev(clen), hq, hkv, d, scale)
+    sync()
+    k8, v8 = host(view.k).reshape(-1, d), host(view.v).reshape(-1, d)
+    ks, vs = host(view.k_scale).reshape(-1), host(view.v_scale).reshape(-1)
+    check_rows(bf16_host(out), q[clen:], k8, v8, ks, vs, clen, sampled_rows(n, 12, n + clen), hq,
+               hkv, d, scale)
+
+
 def test_chunked_prefill_equals_full_tail():
     """Size-independent property: a chunked prefill (cache_len > 0) equals the
     tail rows of one full prefill over the same cache."""
