@@ -53,6 +53,7 @@ constexpr int kCombineThreads = 256;
 constexpr int kCombineSlice   = 32;    // head_dim slice per merge workgroup
 constexpr int kCoopMaxKeys    = 4096;  // contexts up to this run cooperative workgroups
 constexpr int kWideUnits      = 1024;  // fewer (kv head, split) units: one workgroup each
+constexpr int kNtMinTiles     = 8;     // tiles past the first a wave streams with nontemporal loads
 
 template <int D>
 struct DecTraits {
@@ -88,7 +89,19 @@ __device__ __forceinline__ int key_of(int g, int j) {  // P^T k-index -> key in 
     return (j < 4) ? (4 * g + j) : (16 + 4 * g + (j - 4));
 }
 
-template <int D>
+template <bool kNT, typename T>
+__device__ __forceinline__ T ld(const T* p) {
+    if constexpr (kNT) {
+        return __builtin_nontemporal_load(p);
+    } else {
+        return *p;
+    }
+}
+
+// Loads one tile's codes and scales. kNT: the K/V codes (read exactly once
+// per call) use nontemporal loads, which stream faster once a wave has many
+// tiles to read but have a longer latency than plain loads.
+template <int D, bool kNT>
 __device__ __forceinline__ void load_tile(TileRaw<D>& t, const uint8_t* __restrict__ k,
                                           const uint8_t* __restrict__ v,
                                           const float* __restrict__ ks,
@@ -103,7 +116,7 @@ __device__ __forceinline__ void load_tile(TileRaw<D>& t, const uint8_t* __restri
         const uint8_t* kr  = k + (static_cast<int64_t>(key + delta) * hkv + kvh) * D;
 #pragma unroll
         for (int c = 0; c < T::kKChunks; ++c) {
-            t.kraw[u][c] = *reinterpret_cast<const u32x4*>(kr + 16 * g + 64 * c);
+            t.kraw[u][c] = ld<kNT>(reinterpret_cast<const u32x4*>(kr + 16 * g + 64 * c));
         }
     }
 #pragma unroll
@@ -111,13 +124,13 @@ __device__ __forceinline__ void load_tile(TileRaw<D>& t, const uint8_t* __restri
         const int      key = min(kb + key_of(g, j), k1 - 1);
         const uint8_t* vr  = v + (static_cast<int64_t>(key + delta) * hkv + kvh) * D + T::kVBytes * n;
         if constexpr (T::kVWords == 1) {
-            t.vraw[j][0] = *reinterpret_cast<const uint32_t*>(vr);
+            t.vraw[j][0] = ld<kNT>(reinterpret_cast<const uint32_t*>(vr));
         } else if constexpr (T::kVWords == 2) {
-            const u32x2 w = *reinterpret_cast<const u32x2*>(vr);
+            const u32x2 w = ld<kNT>(reinterpret_cast<const u32x2*>(vr));
             t.vraw[j][0]  = w.x;
             t.vraw[j][1]  = w.y;
         } else {
-            const u32x4 w = *reinterpret_cast<const u32x4*>(vr);
+            const u32x4 w = ld<kNT>(reinterpret_cast<const u32x4*>(vr));
             t.vraw[j][0]  = w.x;
             t.vraw[j][1]  = w.y;
             t.vraw[j][2]  = w.z;
@@ -458,7 +471,6 @@ __global__ __launch_bounds__(kDecThreads) void flash_decode_kernel(
     constexpr int kRing     = DecTraits<D>::kRing;
     const int     last_tile = n_tiles - 1;
     if (t_first <= last_tile) {
-        TileRaw<D> ring[kRing];
         auto tile_delta = [&](int kb) {
             if constexpr (kPaged) {
                 return paged_row(kb, block_table, block_shift) - kb;
@@ -466,27 +478,40 @@ __global__ __launch_bounds__(kDecThreads) void flash_decode_kernel(
                 return 0;
             }
         };
+        auto stream = [&]<bool kNT>() {
+            TileRaw<D> ring[kRing];
 #pragma unroll
-        for (int r = 0; r + 1 < kRing; ++r) {
-            const int kb = k0 + min(t_first + r * t_step, last_tile) * kTileKeys;
-            load_tile<D>(ring[r], k, v, ks, vs, kb, k1, kvh, hkv, lane, tile_delta(kb));
-        }
-        for (int t = t_first;; t += kRing * t_step) {
-            bool done = false;
+            for (int r = 0; r + 1 < kRing; ++r) {
+                const int kb = k0 + min(t_first + r * t_step, last_tile) * kTileKeys;
+                load_tile<D, kNT>(ring[r], k, v, ks, vs, kb, k1, kvh, hkv, lane, tile_delta(kb));
+            }
+            for (int t = t_first;; t += kRing * t_step) {
+                bool done = false;
 #pragma unroll
-            for (int r = 0; r < kRing; ++r) {
-                if (!done) {
-                    const int tr = t + r * t_step;
-                    const int kbn = k0 + min(tr + (kRing - 1) * t_step, last_tile) * kTileKeys;
-                    load_tile<D>(ring[(r + kRing - 1) % kRing], k, v, ks, vs, kbn, k1, kvh, hkv,
-                                 lane, tile_delta(kbn));
-                    process(ring[r], k0 + tr * kTileKeys, k1);
-                    done = tr + t_step > last_tile;
+                for (int r = 0; r < kRing; ++r) {
+                    if (!done) {
+                        const int tr  = t + r * t_step;
+                        const int kbn = k0 + min(tr + (kRing - 1) * t_step, last_tile) * kTileKeys;
+                        load_tile<D, kNT>(ring[(r + kRing - 1) % kRing], k, v, ks, vs, kbn, k1,
+                                          kvh, hkv, lane, tile_delta(kbn));
+                        process(ring[r], k0 + tr * kTileKeys, k1);
+                        done = tr + t_step > last_tile;
+                    }
+                }
+                if (done) {
+                    break;
                 }
             }
-            if (done) {
-                break;
-            }
+        };
+        // A wave that streams many tiles on its own (long splits) is
+        // bandwidth-bound: nontemporal loads. Short splits and cooperative
+        // workgroups are latency-bound: plain loads (measured: 128K at 256
+        // splits 56.3 -> 51.8 us with nontemporal loads; 8K at 256 splits
+        // and 128K at 64 cooperative splits 6-8 % slower with them).
+        if (!pt.coop && last_tile - t_first >= kNtMinTiles) {
+            stream.template operator()<true>();
+        } else {
+            stream.template operator()<false>();
         }
     }
 

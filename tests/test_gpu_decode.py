@@ -111,14 +111,29 @@ def test_config3_depths_single_layer(ctx):
     check(got, q, k8, v8, ks, vs, ctx - 1, hq, hkv, d, scale)
 
 
-def test_config5_long_context_per_head_scales():
-    """32Q/8KV, ctx 131072, 64 splits, per-head scales ~U(0.01, 0.1)."""
+@pytest.mark.parametrize("splits", [64, None])
+def test_config5_long_context_per_head_scales(splits):
+    """32Q/8KV, ctx 131072, per-head scales ~U(0.01, 0.1); the config's 64
+    splits (cooperative workgroups) and the default split count (one wave per
+    512-key split: the nontemporal streaming loads)."""
     hq, hkv, d, ctx = 32, 8, 128, 131072
     scale = np.float32(1.0 / np.sqrt(d))
     q = O.normal_bf16((hq, d), 51)
     ph = (O.uniform_f32(hkv, 0.01, 0.1, 52), O.uniform_f32(hkv, 0.01, 0.1, 53))
     _, _, k8, v8, ks, vs = make_cache(ctx, hkv, d, kind="normal", seed=5, per_head_scale=ph)
-    got = gpu_decode(q, k8, v8, ks, vs, ctx - 1, hq, hkv, d, 64, scale)
+    s = splits if splits is not None else R.default_num_splits(hkv)
+    got = gpu_decode(q, k8, v8, ks, vs, ctx - 1, hq, hkv, d, s, scale)
+    check(got, q, k8, v8, ks, vs, ctx - 1, hq, hkv, d, scale)
+
+
+def test_long_splits_ragged_tail():
+    """One wave per 320-key split (the nontemporal loads) with a partial
+    last split: ctx 40000, 128 splits, 24Q/8KV."""
+    hq, hkv, d, ctx = 24, 8, 128, 40000
+    scale = np.float32(1.0 / np.sqrt(d))
+    q = O.normal_bf16((hq, d), 55)
+    _, _, k8, v8, ks, vs = make_cache(ctx, hkv, d, kind="normal", seed=7)
+    got = gpu_decode(q, k8, v8, ks, vs, ctx - 1, hq, hkv, d, 128, scale)
     check(got, q, k8, v8, ks, vs, ctx - 1, hq, hkv, d, scale)
 
 
