@@ -6,13 +6,16 @@
 // O / l. head_dim is 128, as in the reference (:226).
 //
 // MI355X design:
-//  * Workgroup = one q head x (32 x waves) query rows, 32 rows per wave; the
-//    grid puts the longest (last) row blocks first and keeps the q heads of
-//    one kv head on one XCD so their K/V tiles share an L2.
+//  * Workgroup = one q head x (32 x waves) query rows, 32 rows per wave:
+//    8 waves (256 rows, one workgroup per compute unit) when the grid takes
+//    at least two rounds of those, else 4 waves (128 rows, two per compute
+//    unit, heavy and light row blocks paired when the grid is resident in
+//    one round). Longest (last) row blocks first; the q heads of one kv head
+//    on one XCD so their K/V tiles share an L2.
 //  * Keys go in 64-key tiles. The K tile's E4M3 codes are copied unchanged
 //    into LDS by the LDS-DMA loads (global_load_lds_dwordx4, 16-byte chunks
-//    XOR-swizzled by row so the operand reads are bank-conflict free), one
-//    tile ahead, with no registers or VALU work.
+//    XOR-swizzled by row so the operand reads are bank-conflict free), ahead
+//    of use, with no registers or VALU work.
 //  * Scores S^T = K Q^T run on the fp8 MFMA v_mfma_scale_f32_32x32x64_f8f6f4
 //    with A = the raw K codes from LDS and B = Q split exactly into two E4M3
 //    parts: q * 2^a = hi + lo / 16 (a per row, so the row maximum lands in
@@ -26,8 +29,14 @@
 //  * V is dequantized into LDS as f16(code * v_scale), transposed to V^T in
 //    registers (v_perm) before the LDS write, and O^T += V^T P^T runs on
 //    v_mfma_f32_32x32x16_f16 with P^T straight from the score registers.
-//  * Two buffers for K codes, k_scale factors and V^T: tile kt + 1 is loaded
-//    and staged while tile kt is consumed; one barrier per tile.
+//  * Buffers are separate LDS arrays indexed statically (the tile loop is
+//    unrolled), so the compiler sees the LDS-DMA into one buffer and the reads
+//    of another as independent. One barrier per tile, which waits only for
+//    the K copy the next tile needs.
+//  * 8-wave workgroups run two phase-shifted groups so that the softmax
+//    (VALU) of one wave meets the MFMAs of the other wave on its SIMD; the
+//    4-wave workgroups weave the next tile's copies and V staging between
+//    their own MFMAs.
 #include "device_common.hpp"
 #include "launch.hpp"
 
@@ -332,6 +341,147 @@ __global__ __launch_bounds__(kWaves * kWave, 2) void flash_prefill_kernel(
     float m_ref = 0.0f;   // lazy reference maximum of this lane's row (log2 units)
     float l_run = 0.0f;
 
+    // S^T = K Q^T for one tile: per 32-key block, two k-steps of 64 d, each
+    // as hi and lo MFMAs sharing the K operand; all eight K operand reads are
+    // issued before the first MFMA.
+    auto qk = [&](const uint8_t* kbuf, f32x16 (&sc)[2]) {
+        i32x8 ka[2][2];
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) {
+            const int r = 32 * kb + qn;
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                const int   c0 = 4 * j + 2 * h;
+                const u32x4 lo = *reinterpret_cast<const u32x4*>(kbuf + k_chunk(r, c0));
+                const u32x4 hi = *reinterpret_cast<const u32x4*>(kbuf + k_chunk(r, c0 + 1));
+                ka[kb][j] = i32x8{static_cast<int>(lo.x), static_cast<int>(lo.y),
+                                  static_cast<int>(lo.z), static_cast<int>(lo.w),
+                                  static_cast<int>(hi.x), static_cast<int>(hi.y),
+                                  static_cast<int>(hi.z), static_cast<int>(hi.w)};
+            }
+        }
+        sc[0] = f32x16{};
+        sc[1] = f32x16{};
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb) {
+                sc[kb] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
+                    ka[kb][j], qhi[j], sc[kb], 0, 0, 0, kE8M0One, 0, sc_hi);
+            }
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb) {
+                sc[kb] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
+                    ka[kb][j], qlo[j], sc[kb], 0, 0, 0, kE8M0One, 0, sc_lo);
+            }
+        }
+    };
+    // Softmax of tile kt's scores (in place) into the P^T operands:
+    // t = s * (k_scale * scale * log2 e) - m_ref (register r of block kb is key
+    // 32kb + 8(r/4) + 4h + r%4 of the tile), the causal / key-end mask only on
+    // tiles that cross the diagonal or the end of the keys (a wave-uniform
+    // branch), p = 2^t rounded to f16 and the row sum of those f16 values (four
+    // partial sums). Lazy reference maximum (exact): m_ref moves to the row
+    // maximum only on a wave's first tile or when a row sum exceeds 2^15 (some
+    // score more than 15 above m_ref); otherwise the tile needs no max
+    // reduction, no cross-lane step and no rescale of l and O. Every p and l
+    // use the same m_ref, and p <= 2^15 keeps every p inside the f16 range.
+    auto softmax = [&](f32x16 (&sx)[2], const float* kfb, int kt, f16x8 (&pop)[4]) {
+        const int key0 = kt * kBN;
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) {
+#pragma unroll
+            for (int rg = 0; rg < 4; ++rg) {
+                const f32x4 f = *reinterpret_cast<const f32x4*>(kfb + 32 * kb + 8 * rg + 4 * h);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    sx[kb][4 * rg + e] = fmaf(sx[kb][4 * rg + e], f[e], -m_ref);
+                }
+            }
+        }
+        if ((key0 + kBN - 1 > clen + wq0) || (key0 + kBN > total)) {
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb) {
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int kp = key0 + 32 * kb + 8 * (r >> 2) + 4 * h + (r & 3);
+                    if (kp > my_pos || kp >= total) {
+                        sx[kb][r] = -INFINITY;
+                    }
+                }
+            }
+        }
+        float psum  = 0.0f;
+        auto  exp_p = [&]() {
+            float part[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb) {
+#pragma unroll
+                for (int half = 0; half < 2; ++half) {
+                    f16x8 pw;
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const int   r  = 8 * half + 2 * i;
+                        const f16x2 pp = {
+                            static_cast<_Float16>(__builtin_amdgcn_exp2f(sx[kb][r])),
+                            static_cast<_Float16>(__builtin_amdgcn_exp2f(sx[kb][r + 1]))};
+                        part[i] = __builtin_amdgcn_fdot2(pp, f16x2{1.0f16, 1.0f16}, part[i],
+                                                         false);
+                        pw[2 * i]     = pp.x;
+                        pw[2 * i + 1] = pp.y;
+                    }
+                    pop[2 * kb + half] = pw;
+                }
+            }
+            psum = (part[0] + part[1]) + (part[2] + part[3]);
+        };
+        exp_p();
+        if (__any((kt == 0) || !(psum <= 0x1p15f))) {
+            float tmax = -INFINITY;
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb) {
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    tmax = fmaxf(tmax, sx[kb][r]);
+                }
+            }
+            tmax              = wave_xor_max(tmax, 32);
+            const float delta = (tmax == -INFINITY) ? 0.0f : tmax;
+            const float alpha = (kt == 0) ? 1.0f : __builtin_amdgcn_exp2f(-delta);
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb) {
+                sx[kb] -= delta;
+            }
+            m_ref += delta;
+            l_run *= alpha;
+#pragma unroll
+            for (int db = 0; db < 4; ++db) {
+                o[db] *= alpha;
+            }
+            exp_p();
+        }
+        l_run += psum;
+    };
+    // O^T += V^T P^T, the operand reads running four MFMAs ahead.
+    auto pv = [&](const uint16_t* vtb, const f16x8 (&pop)[4]) {
+#pragma unroll
+        for (int db = 0; db < 4; ++db) {
+            const uint16_t* arow = vtb + (32 * db + qn) * kVPitch + 8 * h;
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                const f16x8 va = *reinterpret_cast<const f16x8*>(arow + 16 * t);
+                o[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, pop[t], o[db], 0, 0, 0);
+            }
+        }
+        __builtin_amdgcn_sched_group_barrier(0x100, 4, 2);
+#pragma unroll
+        for (int i = 0; i < 12; ++i) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 2);
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 2);
+        }
+        __builtin_amdgcn_sched_group_barrier(0x008, 4, 2);
+    };
+
     if constexpr (kWaves == 8) {
         // The two waves sharing a SIMD (w and w + 4) run each tile in
         // different phase orders so that one's softmax (VALU) meets the
@@ -342,137 +492,6 @@ __global__ __launch_bounds__(kWaves * kWave, 2) void flash_prefill_kernel(
         // the V^T buffer it has just finished reading.
         const bool late = wave >= kWaves / 2;
         const int  gtid = tid & (kThreads / 2 - 1);   // thread index within the group
-
-        // S^T = K Q^T for one tile (see above); all eight K operand reads
-        // are issued before the first MFMA.
-        auto qk = [&](const uint8_t* kbuf, f32x16 (&sc)[2]) {
-            i32x8 ka[2][2];
-#pragma unroll
-            for (int kb = 0; kb < 2; ++kb) {
-                const int r = 32 * kb + qn;
-#pragma unroll
-                for (int j = 0; j < 2; ++j) {
-                    const int   c0 = 4 * j + 2 * h;
-                    const u32x4 lo = *reinterpret_cast<const u32x4*>(kbuf + k_chunk(r, c0));
-                    const u32x4 hi = *reinterpret_cast<const u32x4*>(kbuf + k_chunk(r, c0 + 1));
-                    ka[kb][j] = i32x8{static_cast<int>(lo.x), static_cast<int>(lo.y),
-                                      static_cast<int>(lo.z), static_cast<int>(lo.w),
-                                      static_cast<int>(hi.x), static_cast<int>(hi.y),
-                                      static_cast<int>(hi.z), static_cast<int>(hi.w)};
-                }
-            }
-            sc[0] = f32x16{};
-            sc[1] = f32x16{};
-#pragma unroll
-            for (int j = 0; j < 2; ++j) {
-#pragma unroll
-                for (int kb = 0; kb < 2; ++kb) {
-                    sc[kb] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
-                        ka[kb][j], qhi[j], sc[kb], 0, 0, 0, kE8M0One, 0, sc_hi);
-                }
-#pragma unroll
-                for (int kb = 0; kb < 2; ++kb) {
-                    sc[kb] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
-                        ka[kb][j], qlo[j], sc[kb], 0, 0, 0, kE8M0One, 0, sc_lo);
-                }
-            }
-        };
-        // Softmax of tile kt's scores into the P^T operands (see above).
-        auto softmax = [&](f32x16 (&sx)[2], const float* kfb, int kt, f16x8 (&pop)[4]) {
-            const int key0 = kt * kBN;
-#pragma unroll
-            for (int kb = 0; kb < 2; ++kb) {
-#pragma unroll
-                for (int rg = 0; rg < 4; ++rg) {
-                    const f32x4 f = *reinterpret_cast<const f32x4*>(kfb + 32 * kb + 8 * rg + 4 * h);
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        sx[kb][4 * rg + e] = fmaf(sx[kb][4 * rg + e], f[e], -m_ref);
-                    }
-                }
-            }
-            if ((key0 + kBN - 1 > clen + wq0) || (key0 + kBN > total)) {
-#pragma unroll
-                for (int kb = 0; kb < 2; ++kb) {
-#pragma unroll
-                    for (int r = 0; r < 16; ++r) {
-                        const int kp = key0 + 32 * kb + 8 * (r >> 2) + 4 * h + (r & 3);
-                        if (kp > my_pos || kp >= total) {
-                            sx[kb][r] = -INFINITY;
-                        }
-                    }
-                }
-            }
-            float psum  = 0.0f;
-            auto  exp_p = [&]() {
-                float part[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-                for (int kb = 0; kb < 2; ++kb) {
-#pragma unroll
-                    for (int half = 0; half < 2; ++half) {
-                        f16x8 pw;
-#pragma unroll
-                        for (int i = 0; i < 4; ++i) {
-                            const int   r  = 8 * half + 2 * i;
-                            const f16x2 pp = {
-                                static_cast<_Float16>(__builtin_amdgcn_exp2f(sx[kb][r])),
-                                static_cast<_Float16>(__builtin_amdgcn_exp2f(sx[kb][r + 1]))};
-                            part[i] = __builtin_amdgcn_fdot2(pp, f16x2{1.0f16, 1.0f16}, part[i],
-                                                             false);
-                            pw[2 * i]     = pp.x;
-                            pw[2 * i + 1] = pp.y;
-                        }
-                        pop[2 * kb + half] = pw;
-                    }
-                }
-                psum = (part[0] + part[1]) + (part[2] + part[3]);
-            };
-            exp_p();
-            if (__any((kt == 0) || !(psum <= 0x1p15f))) {
-                float tmax = -INFINITY;
-#pragma unroll
-                for (int kb = 0; kb < 2; ++kb) {
-#pragma unroll
-                    for (int r = 0; r < 16; ++r) {
-                        tmax = fmaxf(tmax, sx[kb][r]);
-                    }
-                }
-                tmax              = wave_xor_max(tmax, 32);
-                const float delta = (tmax == -INFINITY) ? 0.0f : tmax;
-                const float alpha = (kt == 0) ? 1.0f : __builtin_amdgcn_exp2f(-delta);
-#pragma unroll
-                for (int kb = 0; kb < 2; ++kb) {
-                    sx[kb] -= delta;
-                }
-                m_ref += delta;
-                l_run *= alpha;
-#pragma unroll
-                for (int db = 0; db < 4; ++db) {
-                    o[db] *= alpha;
-                }
-                exp_p();
-            }
-            l_run += psum;
-        };
-        // O^T += V^T P^T, the operand reads running four MFMAs ahead.
-        auto pv = [&](const uint16_t* vtb, const f16x8 (&pop)[4]) {
-#pragma unroll
-            for (int db = 0; db < 4; ++db) {
-                const uint16_t* arow = vtb + (32 * db + qn) * kVPitch + 8 * h;
-#pragma unroll
-                for (int t = 0; t < 4; ++t) {
-                    const f16x8 va = *reinterpret_cast<const f16x8*>(arow + 16 * t);
-                    o[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, pop[t], o[db], 0, 0, 0);
-                }
-            }
-            __builtin_amdgcn_sched_group_barrier(0x100, 4, 2);
-#pragma unroll
-            for (int i = 0; i < 12; ++i) {
-                __builtin_amdgcn_sched_group_barrier(0x008, 1, 2);
-                __builtin_amdgcn_sched_group_barrier(0x100, 1, 2);
-            }
-            __builtin_amdgcn_sched_group_barrier(0x008, 4, 2);
-        };
 
         constexpr int kGThreads = kThreads / 2;
         constexpr int kGReps    = 4096 / 8 / kGThreads;
@@ -584,7 +603,7 @@ __global__ __launch_bounds__(kWaves * kWave, 2) void flash_prefill_kernel(
             v_tile_load<kThreads>(raw1, v, ks, vs, r1, kvh, hkv, tid);
         }
         __syncthreads();
-    
+
         // Rows of the tiles one and two ahead, looked up (paged) a tile
         // before use.
         TileRows<kPaged> rn1(kBN, total, block_table, block_shift);
@@ -616,15 +635,15 @@ __global__ __launch_bounds__(kWaves * kWave, 2) void flash_prefill_kernel(
                 const int key0 = kt * kBN;
                 k_tile_dma<kThreads>(nk, k, r1, kvh, hkv, tid);
                 v_tile_load<kThreads>(rawc, v, ks, vs, r2, kvh, hkv, tid);
-    
+
                 // S^T = K Q^T: per 32-key block, two k-steps of 64 d, each as
                 // hi and lo MFMAs sharing the K operand.
                 f32x16 s[2];
-    #pragma unroll
+#pragma unroll
                 for (int kb = 0; kb < 2; ++kb) {
                     s[kb] = f32x16{};
                     const int r = 32 * kb + qn;
-    #pragma unroll
+#pragma unroll
                     for (int j = 0; j < 2; ++j) {
                         const int c0 = 4 * j + 2 * h;
                         const u32x4 lo = *reinterpret_cast<const u32x4*>(kt_s + k_chunk(r, c0));
@@ -639,114 +658,29 @@ __global__ __launch_bounds__(kWaves * kWave, 2) void flash_prefill_kernel(
                             ka, qlo[j], s[kb], 0, 0, 0, kE8M0One, 0, sc_lo);
                     }
                 }
-    #pragma unroll
+#pragma unroll
                 for (int i = 0; i < 8; ++i) {
                     __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
                     __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);   // LDS read
                     __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);   // VALU
                     __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);   // global load
                 }
-    
-                // t = s * (k_scale * scale * log2 e) - m_ref, one fma per score.
-                // Register r of block kb is key 32kb + 8(r/4) + 4h + r%4 of the tile.
-    #pragma unroll
-                for (int kb = 0; kb < 2; ++kb) {
-    #pragma unroll
-                    for (int rg = 0; rg < 4; ++rg) {
-                        const f32x4 f = *reinterpret_cast<const f32x4*>(kf + 32 * kb + 8 * rg + 4 * h);
-    #pragma unroll
-                        for (int e = 0; e < 4; ++e) {
-                            s[kb][4 * rg + e] = fmaf(s[kb][4 * rg + e], f[e], -m_ref);
-                        }
-                    }
-                }
-                // Causal / key-end mask, only on tiles that cross the diagonal or
-                // the end of the keys (a wave-uniform branch).
-                if ((key0 + kBN - 1 > clen + wq0) || (key0 + kBN > total)) {
-    #pragma unroll
-                    for (int kb = 0; kb < 2; ++kb) {
-    #pragma unroll
-                        for (int r = 0; r < 16; ++r) {
-                            const int kp = key0 + 32 * kb + 8 * (r >> 2) + 4 * h + (r & 3);
-                            if (kp > my_pos || kp >= total) {
-                                s[kb][r] = -INFINITY;
-                            }
-                        }
-                    }
-                }
-    
-                // p = 2^t rounded to f16 (the P^T operands), and the row sum of
-                // those f16 values.
+
                 f16x8 pop[4];
-                float psum  = 0.0f;
-                auto  exp_p = [&]() {
-                    float part[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-    #pragma unroll
-                    for (int kb = 0; kb < 2; ++kb) {
-    #pragma unroll
-                        for (int half = 0; half < 2; ++half) {
-                            f16x8 pw;
-    #pragma unroll
-                            for (int i = 0; i < 4; ++i) {
-                                const int   r  = 8 * half + 2 * i;
-                                const f16x2 pp = {
-                                    static_cast<_Float16>(__builtin_amdgcn_exp2f(s[kb][r])),
-                                    static_cast<_Float16>(__builtin_amdgcn_exp2f(s[kb][r + 1]))};
-                                part[i] = __builtin_amdgcn_fdot2(pp, f16x2{1.0f16, 1.0f16}, part[i], false);
-                                pw[2 * i]     = pp.x;
-                                pw[2 * i + 1] = pp.y;
-                            }
-                            pop[2 * kb + half] = pw;
-                        }
-                    }
-                    psum = (part[0] + part[1]) + (part[2] + part[3]);
-                };
-                exp_p();
-                // Lazy reference maximum (exact): m_ref moves to the row maximum
-                // only on a wave's first tile or when a row sum exceeds 2^15 (some
-                // score more than 15 above m_ref); otherwise the tile needs no max
-                // reduction, no cross-lane step and no accumulator rescale. Every
-                // p and l use the same m_ref, and p <= 2^15 keeps every p inside
-                // the f16 range.
-                if (__any((kt == 0) || !(psum <= 0x1p15f))) {
-                    float tmax = -INFINITY;
-    #pragma unroll
-                    for (int kb = 0; kb < 2; ++kb) {
-    #pragma unroll
-                        for (int r = 0; r < 16; ++r) {
-                            tmax = fmaxf(tmax, s[kb][r]);
-                        }
-                    }
-                    tmax              = wave_xor_max(tmax, 32);
-                    const float delta = (tmax == -INFINITY) ? 0.0f : tmax;
-                    // On the first tile l and O are still zero (and 2^-delta may be inf).
-                    const float alpha = (kt == 0) ? 1.0f : __builtin_amdgcn_exp2f(-delta);
-    #pragma unroll
-                    for (int kb = 0; kb < 2; ++kb) {
-                        s[kb] -= delta;
-                    }
-                    m_ref += delta;
-                    l_run *= alpha;
-    #pragma unroll
-                    for (int db = 0; db < 4; ++db) {
-                        o[db] *= alpha;
-                    }
-                    exp_p();
-                }
-                l_run += psum;
-    
+                softmax(s, kf, kt, pop);
+
                 // O^T += V^T P^T.
-    #pragma unroll
+#pragma unroll
                 for (int db = 0; db < 4; ++db) {
                     const uint16_t* arow = vt + (32 * db + qn) * kVPitch + 8 * h;
-    #pragma unroll
+#pragma unroll
                     for (int t = 0; t < 4; ++t) {
                         const f16x8 va = *reinterpret_cast<const f16x8*>(arow + 16 * t);
                         o[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, pop[t], o[db], 0, 0, 0);
                     }
                 }
                 v_tile_stage<kThreads>(rawn, nvt, nkf, tid, scale_log2);
-    #pragma unroll
+#pragma unroll
                 for (int i = 0; i < 16; ++i) {
                     __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);   // MFMA
                     __builtin_amdgcn_sched_group_barrier(0x100, 1, 1);   // LDS read
@@ -763,14 +697,14 @@ __global__ __launch_bounds__(kWaves * kWave, 2) void flash_prefill_kernel(
             __builtin_amdgcn_s_waitcnt(kWaitAllButVLoads);
             lds_barrier();
         };
-    
+
         for (int kt = 0; kt < n_tiles; kt += 2) {
             tile.template operator()<0>(kt);
             if (kt + 1 < n_tiles) {
                 tile.template operator()<1>(kt + 1);
             }
         }
-    
+
     }
 
     const float l_tot = wave_xor_sum(l_run, 32);
