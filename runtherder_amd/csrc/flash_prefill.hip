@@ -307,10 +307,14 @@ __global__ __launch_bounds__(kWaves * kWave, 2) void flash_prefill_kernel(
         }
         amax = wave_xor_max(amax, 32);
         // 2^a with amax * 2^a in [128, 256); a zero row keeps a = 0.
-        const int a = (amax > 0.0f) ? 7 - (static_cast<int>(pow2_bits(amax) >> 23) - 127) : 0;
+        // (a is clamped so that 2^a, 2^-a and 2^(-a-4) stay normal: only rows
+        // with max |q| below 2^-116 land under 128.)
+        const int a = (amax > 0.0f)
+                          ? min(max(7 - (static_cast<int>(pow2_bits(amax) >> 23) - 127), -120), 123)
+                          : 0;
         const float s2a = __uint_as_float(static_cast<uint32_t>(127 + a) << 23);
-        sc_hi = min(max(kE8M0One - a, 0), 254);
-        sc_lo = min(max(kE8M0One - a - 4, 0), 254);
+        sc_hi = kE8M0One - a;
+        sc_lo = kE8M0One - a - 4;
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
 #pragma unroll
@@ -445,8 +449,13 @@ __global__ __launch_bounds__(kWaves * kWave, 2) void flash_prefill_kernel(
                     tmax = fmaxf(tmax, sx[kb][r]);
                 }
             }
-            tmax              = wave_xor_max(tmax, 32);
-            const float delta = (tmax == -INFINITY) ? 0.0f : tmax;
+            tmax = wave_xor_max(tmax, 32);
+            // The first tile sets the reference; later tiles only raise it. A
+            // row that is here because another row of the wave overflowed may
+            // sit far below its reference: lowering it would scale O and l by
+            // 2^-tmax, which overflows.
+            const float delta = (kt == 0) ? ((tmax == -INFINITY) ? 0.0f : tmax)
+                                          : fmaxf(tmax, 0.0f);
             const float alpha = (kt == 0) ? 1.0f : __builtin_amdgcn_exp2f(-delta);
 #pragma unroll
             for (int kb = 0; kb < 2; ++kb) {
