@@ -75,6 +75,22 @@ def test_split_count_sweep(splits):
     check(got, q, k8, v8, ks, vs, cache_len, hq, hkv, d, scale)
 
 
+@pytest.mark.parametrize("splits", [1, 16, 64])
+def test_q_heads_of_extreme_magnitude(splits):
+    """q heads scaled from zero and bf16 subnormals up to 2^6: scores several
+    hundred apart across tiles and splits must raise the running maximum
+    without overflow, and near-zero heads give the mean of V."""
+    hq, hkv, d, cache_len = 32, 8, 128, 4999
+    scale = np.float32(1.0 / np.sqrt(d))
+    f = np.tile(np.array([0.0, 2.0**-130, 2.0**-121, 2.0**-60, 1.0, 2.0**3, 2.0**5, 2.0**6],
+                         dtype=np.float32), hq // 8)
+    q = O.f32_to_bf16(O.bf16_to_f32(O.normal_bf16((hq, d), 77)) * f[:, None])
+    _, _, k8, v8, ks, vs = make_cache(cache_len + 1, hkv, d, kind="normal", seed=7)
+    got = gpu_decode(q, k8, v8, ks, vs, cache_len, hq, hkv, d, splits, scale)
+    assert np.isfinite(O.bf16_to_f32(got)).all()
+    check(got, q, k8, v8, ks, vs, cache_len, hq, hkv, d, scale)
+
+
 def test_config1_per_tensor_scale():
     """24Q/8KV, D 128, ctx 511; K/V N(0,1) quantized with one per-tensor
     scale amax/448 broadcast into the per-(token, kv_head) slab."""
