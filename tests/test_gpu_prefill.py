@@ -208,6 +208,27 @@ def test_large_grid_ragged_tile_counts(clen):
                hkv, d, scale)
 
 
+@pytest.mark.parametrize("hq,hkv", [(64, 64), (64, 4)])
+def test_large_grid_group_sizes(hq, hkv):
+    """The 8-wave path (ceil(2100 / 256) * 64 heads fills two rounds) with
+    GQA groups of 1 and 16 q heads per kv head and a cache offset. Oracle on
+    sampled rows."""
+    d, n, clen = 128, 2100, 50
+    total = clen + n
+    scale = np.float32(1.0 / np.sqrt(d))
+    q, k, v = rope_qkv(total, hq, hkv, d, 1e6, False, 7000 + hkv)
+    cache, view = append_and_check(0, k, v, hkv, d, total)
+    out = torch.empty((n, hq, d), dtype=torch.bfloat16, device=DEV)
+    step(f"group-size prefill n={n} clen={clen} hq={hq} hkv={hkv}")
+    R.flash_prefill_bf16(out, bf16_dev(q[clen:]), view.k, view.v, view.k_scale, view.v_scale, n,
+                         int_dev(clen), hq, hkv, d, scale)
+    sync()
+    k8, v8 = host(view.k).reshape(-1, d), host(view.v).reshape(-1, d)
+    ks, vs = host(view.k_scale).reshape(-1), host(view.v_scale).reshape(-1)
+    check_rows(bf16_host(out), q[clen:], k8, v8, ks, vs, clen, sampled_rows(n, 10, n + hkv), hq,
+               hkv, d, scale)
+
+
 def test_chunked_prefill_equals_full_tail():
     """Size-independent property: a chunked prefill (cache_len > 0) equals the
     tail rows of one full prefill over the same cache."""
