@@ -155,7 +155,7 @@ int rth_rope_append_fp8(uint16_t* q, uint8_t* k_cache, uint8_t* v_cache,
                         void* stream);
 
 /* Paged KV cache (no counterpart in the reference, whose README plans paged
- * attention; SURVEY next item 3): the cache slabs hold physical blocks of
+ * attention, README.md:142-143): the cache slabs hold physical blocks of
  * block_size positions ([num_blocks * block_size, Hkv, D] E4M3 and
  * [num_blocks * block_size, Hkv] fp32 scales); logical position p of the
  * sequence lives at physical position block_table[p / block_size] *
