@@ -1,7 +1,8 @@
 """Paged KV layout (no reference counterpart; the reference README plans paged
-attention, README.md:142-143): a paged cache with a shuffled block table must hold, after gathering, the bytes the
-contiguous cache holds, and decode / fused append+decode / prefill over it
-must return exactly the contiguous results (same data, same order of work)."""
+attention, README.md:142-143): a paged cache with a shuffled block table must
+hold, after gathering, the bytes the contiguous cache holds, and decode /
+fused append+decode / prefill over it must return exactly the contiguous
+results (same data, same order of work)."""
 import numpy as np
 import pytest
 import torch
