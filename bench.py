@@ -60,6 +60,24 @@ class EventTimer:
         self.ms = self.a.elapsed_time(self.b)
 
 
+def graph_us(torch, stream, fn, iters):
+    """Microseconds per call of fn, captured iters times in one HIP graph and
+    timed over a replay (one warm replay first): the kernels back to back,
+    without the host launch rate of an eager loop."""
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(stream):
+        fn()
+        torch.cuda.synchronize()
+        with torch.cuda.graph(g, stream=stream):
+            for _ in range(iters):
+                fn()
+        g.replay()
+        with EventTimer(torch, stream) as t:
+            g.replay()
+    torch.cuda.synchronize()
+    return t.ms * 1e3 / iters
+
+
 def bench_decode(torch, R, args, stream):
     hq, hkv, d, L = 24, 8, 128, 28
     ctx0 = args.ctx                          # keys attended at the first step
@@ -189,14 +207,11 @@ def bench_prefill(torch, R, stream, n=4096, iters=None):
             for _ in range(iters):
                 R.flash_prefill_bf16(out, q, view.k, view.v, view.k_scale, view.v_scale, n,
                                      pos, hq, hkv, d, scale)
-        with EventTimer(torch, stream) as ta:
-            for _ in range(iters):
-                cache.append(0, k, v, n, pos)
     torch.cuda.synchronize()
     us = t.ms * 1e3 / iters
     fl = prefill_flops(n, 0, hq, d)
     tflops = fl / (us * 1e-6) / 1e12
-    app_us = ta.ms * 1e3 / iters
+    app_us = graph_us(torch, stream, lambda: cache.append(0, k, v, n, pos), 50)
     app_bytes = n * hkv * d * 4 + n * hkv * d * 2 + n * hkv * 8
     return {"n": n, "us": us, "flops": fl, "tflops": tflops, "append_us": app_us,
             "append_gbs": app_bytes / (app_us * 1e-6) / 1e9}
@@ -240,17 +255,10 @@ def bench_rope_append(torch, R, stream, n=4096, iters=20):
         def qwen_fused():
             cache.append_qk_norm_rope(0, q, k, v, n, qn, kn, eps, positions, inv, pos, hq)
 
-        res = {}
-        for name, fn in (("two_step_us", llama_two_step), ("fused_us", llama_fused),
-                         ("qwen_unfused_us", qwen_unfused), ("qwen_fused_us", qwen_fused)):
-            for _ in range(2):
-                fn()
-            torch.cuda.synchronize()
-            with EventTimer(torch, stream) as t:
-                for _ in range(iters):
-                    fn()
-            res[name] = round(t.ms * 1e3 / iters, 2)
-    torch.cuda.synchronize()
+    res = {}
+    for name, fn in (("two_step_us", llama_two_step), ("fused_us", llama_fused),
+                     ("qwen_unfused_us", qwen_unfused), ("qwen_fused_us", qwen_fused)):
+        res[name] = round(graph_us(torch, stream, fn, iters), 2)
     fused_bytes = n * hq * d * 4 + n * hkv * d * 4 + n * hkv * d * 2 + n * hkv * 8
     res.update({"n": n, "fused_bytes": fused_bytes,
                 "fused_gbs": round(fused_bytes / (res["fused_us"] * 1e-6) / 1e9, 1),
