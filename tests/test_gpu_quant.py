@@ -44,6 +44,24 @@ def test_quantize_normal_wide_range_bit_exact():
     assert np.array_equal(q, wq)
 
 
+@pytest.mark.parametrize("rows,d", [(33001, 128), (32770, 256)])
+def test_large_append_half_lanes_bit_exact(rows, d):
+    """Appends of 32768 rows or more run with half the lanes per row (two
+    loads in flight per lane); ragged row counts, wide-range values and
+    zero / NaN / inf rows must still match the oracle bit for bit."""
+    x = O.normal_bf16((rows, d), 123 + d)
+    x[::5] = O.f32_to_bf16(O.bf16_to_f32(x[::5]) * np.float32(1e-3))
+    x[2::9] = O.f32_to_bf16(O.bf16_to_f32(x[2::9]) * np.float32(3e4))
+    x[rows - 1] = 0
+    x[rows - 2] = 0x8000
+    x[rows - 3, 17] = 0x7FC0
+    x[rows - 4, 5] = 0x7F80
+    q, s = run_quant(x, d)
+    wq, ws = O.quantize_kv_fp8(x, d)
+    assert np.array_equal(s.view(np.uint32), ws.view(np.uint32))
+    assert np.array_equal(q, wq)
+
+
 def test_zero_nan_inf_rows():
     x = O.normal_bf16((4, 128), 9)
     x[0] = 0
