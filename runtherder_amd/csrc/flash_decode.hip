@@ -63,7 +63,9 @@ struct DecTraits {
     static constexpr int kVBytes  = D / 16;   // V bytes per lane per key
     static constexpr int kVWords  = kVBytes / 4;
     static constexpr int kOMfma   = D / 16;   // PV MFMAs, one per d offset c
-    static constexpr int kRing    = 2;  // register tiles in flight (deeper measured slower)
+    // Register tiles in the ring (deeper measured slower); D 256 tiles are
+    // 65 registers each, so that width keeps one (two spill).
+    static constexpr int kRing    = (D == 256) ? 1 : 2;
 };
 
 // Physical cache row of logical key `key` when the cache is paged: blocks of
