@@ -221,16 +221,20 @@ constexpr int waitcnt_vm(int n) {
     return (n & 0xf) | (0x7 << 4) | (0xf << 8) | ((n >> 4) << 14);
 }
 
-template <int kWaves, bool kPaged>
-__global__ __launch_bounds__(kWaves * kWave, 2) void flash_prefill_kernel(
+template <int kWaves, bool kPaged, bool kSplit = false>
+__global__ __launch_bounds__(kWaves * kWave, kSplit ? 1 : 2) void flash_prefill_kernel(
     uint16_t* __restrict__ out, const uint16_t* __restrict__ q,
     const uint8_t* __restrict__ k, const uint8_t* __restrict__ v,
     const float* __restrict__ ks, const float* __restrict__ vs, int n_new,
     const int* __restrict__ cache_len, int hq, int hkv, float scale_log2,
     const int* __restrict__ block_table, int block_shift, bool one_round) {
+    static_assert(!kSplit || kWaves == 8, "the key split pairs two 4-wave halves");
     constexpr int kThreads = kWaves * kWave;
-    constexpr int kBM      = 32 * kWaves;           // query rows per workgroup
-    constexpr int kReps    = 4096 / 8 / kThreads;   // V staging units per thread
+    constexpr int kRowWaves = kSplit ? 4 : kWaves;  // waves with distinct rows
+    constexpr int kBM      = 32 * kRowWaves;        // query rows per workgroup
+    // Threads of one tile pipeline (the whole workgroup, or one split half).
+    constexpr int kPThreads = kSplit ? kThreads / 2 : kThreads;
+    constexpr int kReps    = 4096 / 8 / kPThreads;  // V staging units per thread
     // Vector-memory operations of one v_tile_load (4 per unit, 1 k_scale).
     constexpr int kWaitAllButVLoads = waitcnt_vm(4 * kReps + 1);
 
@@ -245,6 +249,10 @@ __global__ __launch_bounds__(kWaves * kWave, 2) void flash_prefill_kernel(
     __shared__ __attribute__((aligned(16))) uint16_t sVt1[kHD * kVPitch];
     __shared__ __attribute__((aligned(16))) float    sKf0[kBN];
     __shared__ __attribute__((aligned(16))) float    sKf1[kBN];
+    __shared__ __attribute__((aligned(16))) uint16_t sVt2[kHD * kVPitch];   // key split only
+    __shared__ __attribute__((aligned(16))) uint16_t sVt3[kHD * kVPitch];   // key split only
+    __shared__ __attribute__((aligned(16))) float    sKf2[kBN];             // key split only
+    __shared__ __attribute__((aligned(16))) float    sKf3[kBN];             // key split only
 
     const int tid  = static_cast<int>(threadIdx.x);
     const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
@@ -272,7 +280,10 @@ __global__ __launch_bounds__(kWaves * kWave, 2) void flash_prefill_kernel(
     const int last    = min(q0 + kBM, n_new) - 1;
     const int n_tiles = min((total + kBN - 1) / kBN, (clen + last) / kBN + 1);
 
-    const int wq0     = q0 + wave * 32;              // first row of this wave
+    // Key split: waves w and w + 4 hold the same rows; half g = w / 4 runs
+    // the key tiles kt = g, g + 2, g + 4, ... and the halves merge at the end.
+    const int split_g = kSplit ? (wave >> 2) : 0;
+    const int wq0     = q0 + (kSplit ? (wave & 3) : wave) * 32;   // first row of this wave
     const int wlast   = min(wq0 + 31, n_new - 1);    // may be < wq0 (idle wave)
     const int w_tiles = (wlast < wq0) ? 0 : (clen + wlast) / kBN + 1;
     const int my_q    = wq0 + qn;
@@ -440,7 +451,7 @@ __global__ __launch_bounds__(kWaves * kWave, 2) void flash_prefill_kernel(
             psum = (part[0] + part[1]) + (part[2] + part[3]);
         };
         exp_p();
-        if (__any((kt == 0) || !(psum <= 0x1p15f))) {
+        if (__any((kt == split_g) || !(psum <= 0x1p15f))) {
             float tmax = -INFINITY;
 #pragma unroll
             for (int kb = 0; kb < 2; ++kb) {
@@ -454,9 +465,9 @@ __global__ __launch_bounds__(kWaves * kWave, 2) void flash_prefill_kernel(
             // row that is here because another row of the wave overflowed may
             // sit far below its reference: lowering it would scale O and l by
             // 2^-tmax, which overflows.
-            const float delta = (kt == 0) ? ((tmax == -INFINITY) ? 0.0f : tmax)
+            const float delta = (kt == split_g) ? ((tmax == -INFINITY) ? 0.0f : tmax)
                                           : fmaxf(tmax, 0.0f);
-            const float alpha = (kt == 0) ? 1.0f : __builtin_amdgcn_exp2f(-delta);
+            const float alpha = (kt == split_g) ? 1.0f : __builtin_amdgcn_exp2f(-delta);
 #pragma unroll
             for (int kb = 0; kb < 2; ++kb) {
                 sx[kb] -= delta;
@@ -491,7 +502,7 @@ __global__ __launch_bounds__(kWaves * kWave, 2) void flash_prefill_kernel(
         __builtin_amdgcn_sched_group_barrier(0x008, 4, 2);
     };
 
-    if constexpr (kWaves == 8) {
+    if constexpr (kWaves == 8 && !kSplit) {
         // The two waves sharing a SIMD (w and w + 4) run each tile in
         // different phase orders so that one's softmax (VALU) meets the
         // other's MFMAs: the early group (waves 0-3) copies the next K tile
@@ -597,34 +608,48 @@ __global__ __launch_bounds__(kWaves * kWave, 2) void flash_prefill_kernel(
             }
         }
     } else {
+    // One tile pipeline per half G (the whole workgroup unless key split):
+    // the stream of tiles G, G + kStride, G + 2 kStride, ... Each half has its
+    // own LDS buffers; both halves take the same number of barriers.
+    constexpr int kStride = kSplit ? 2 : 1;
+    const int     ptid    = tid & (kPThreads - 1);   // thread index within the pipeline
+    auto pipeline = [&]<int G>() {
     // V staging registers, two sets: raw0 holds the even tiles, raw1 the odd
         // ones, so the loads of tile kt + 2 go out a whole tile before the
         // staging of tile kt + 1 needs its registers.
-        // Prologue: tile 0 staged, K(1) copied, V(1) in raw1.
+        // Prologue: the stream's first tile staged, the second's K copied
+        // and V in raw1. (Tile "kt + 1" below is the stream's next tile,
+        // kt + kStride.)
         VRaw<kReps> raw0, raw1;
         {
-            const TileRows<kPaged> r0(0, total, block_table, block_shift);
-            const TileRows<kPaged> r1(kBN, total, block_table, block_shift);
-            k_tile_dma<kThreads>(sK0, k, r0, kvh, hkv, tid);
-            v_tile_load<kThreads>(raw0, v, ks, vs, r0, kvh, hkv, tid);
-            v_tile_stage<kThreads>(raw0, sVt0, sKf0, tid, scale_log2);
-            k_tile_dma<kThreads>(sK1, k, r1, kvh, hkv, tid);
-            v_tile_load<kThreads>(raw1, v, ks, vs, r1, kvh, hkv, tid);
+            const TileRows<kPaged> r0(G * kBN, total, block_table, block_shift);
+            const TileRows<kPaged> r1((G + kStride) * kBN, total, block_table, block_shift);
+            k_tile_dma<kPThreads>(G ? sK2 : sK0, k, r0, kvh, hkv, ptid);
+            v_tile_load<kPThreads>(raw0, v, ks, vs, r0, kvh, hkv, ptid);
+            v_tile_stage<kPThreads>(raw0, G ? sVt2 : sVt0, G ? sKf2 : sKf0, ptid, scale_log2);
+            k_tile_dma<kPThreads>(G ? sK3 : sK1, k, r1, kvh, hkv, ptid);
+            v_tile_load<kPThreads>(raw1, v, ks, vs, r1, kvh, hkv, ptid);
         }
         __syncthreads();
 
         // Rows of the tiles one and two ahead, looked up (paged) a tile
         // before use.
-        TileRows<kPaged> rn1(kBN, total, block_table, block_shift);
-        TileRows<kPaged> rn2(2 * kBN, total, block_table, block_shift);
+        TileRows<kPaged> rn1((G + kStride) * kBN, total, block_table, block_shift);
+        TileRows<kPaged> rn2((G + 2 * kStride) * kBN, total, block_table, block_shift);
         // One tile from buffer B (static, so each buffer is a distinct array).
         auto tile = [&]<int B>(int kt) {
-            uint8_t*  kt_s = B ? sK1 : sK0;
-            uint16_t* vt   = B ? sVt1 : sVt0;
-            float*    kf   = B ? sKf1 : sKf0;
-            uint8_t*  nk   = B ? sK0 : sK1;
-            uint16_t* nvt  = B ? sVt0 : sVt1;
-            float*    nkf  = B ? sKf0 : sKf1;
+            uint8_t*  kb0 = G ? sK2 : sK0;
+            uint8_t*  kb1 = G ? sK3 : sK1;
+            uint16_t* vb0 = G ? sVt2 : sVt0;
+            uint16_t* vb1 = G ? sVt3 : sVt1;
+            float*    fb0 = G ? sKf2 : sKf0;
+            float*    fb1 = G ? sKf3 : sKf1;
+            uint8_t*  kt_s = B ? kb1 : kb0;
+            uint16_t* vt   = B ? vb1 : vb0;
+            float*    kf   = B ? fb1 : fb0;
+            uint8_t*  nk   = B ? kb0 : kb1;
+            uint16_t* nvt  = B ? vb0 : vb1;
+            float*    nkf  = B ? fb0 : fb1;
             // On entry V(kt + 1) is in registers rawn (loaded during tile
             // kt - 1). This tile copies K(kt + 1) into K buffer 1 - B, loads
             // V(kt + 2) into rawc (issued after the copy, so that waiting for
@@ -639,11 +664,10 @@ __global__ __launch_bounds__(kWaves * kWave, 2) void flash_prefill_kernel(
             const TileRows<kPaged> r1 = rn1;
             const TileRows<kPaged> r2 = rn2;
             rn1 = rn2;
-            rn2 = TileRows<kPaged>((kt + 3) * kBN, total, block_table, block_shift);
+            rn2 = TileRows<kPaged>((kt + 3 * kStride) * kBN, total, block_table, block_shift);
             if (kt < w_tiles) {
-                const int key0 = kt * kBN;
-                k_tile_dma<kThreads>(nk, k, r1, kvh, hkv, tid);
-                v_tile_load<kThreads>(rawc, v, ks, vs, r2, kvh, hkv, tid);
+                k_tile_dma<kPThreads>(nk, k, r1, kvh, hkv, ptid);
+                v_tile_load<kPThreads>(rawc, v, ks, vs, r2, kvh, hkv, ptid);
 
                 // S^T = K Q^T: per 32-key block, two k-steps of 64 d, each as
                 // hi and lo MFMAs sharing the K operand.
@@ -688,7 +712,7 @@ __global__ __launch_bounds__(kWaves * kWave, 2) void flash_prefill_kernel(
                         o[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, pop[t], o[db], 0, 0, 0);
                     }
                 }
-                v_tile_stage<kThreads>(rawn, nvt, nkf, tid, scale_log2);
+                v_tile_stage<kPThreads>(rawn, nvt, nkf, ptid, scale_log2);
 #pragma unroll
                 for (int i = 0; i < 16; ++i) {
                     __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);   // MFMA
@@ -697,9 +721,9 @@ __global__ __launch_bounds__(kWaves * kWave, 2) void flash_prefill_kernel(
                     __builtin_amdgcn_sched_group_barrier(0x200, 1, 1);   // LDS write
                 }
             } else {
-                k_tile_dma<kThreads>(nk, k, r1, kvh, hkv, tid);
-                v_tile_load<kThreads>(rawc, v, ks, vs, r2, kvh, hkv, tid);
-                v_tile_stage<kThreads>(rawn, nvt, nkf, tid, scale_log2);
+                k_tile_dma<kPThreads>(nk, k, r1, kvh, hkv, ptid);
+                v_tile_load<kPThreads>(rawc, v, ks, vs, r2, kvh, hkv, ptid);
+                v_tile_stage<kPThreads>(rawn, nvt, nkf, ptid, scale_log2);
             }
             // K(kt + 1) must have landed and the staged LDS writes be visible
             // before the next tile; the V loads of tile kt + 2 stay in flight.
@@ -707,13 +731,60 @@ __global__ __launch_bounds__(kWaves * kWave, 2) void flash_prefill_kernel(
             lds_barrier();
         };
 
-        for (int kt = 0; kt < n_tiles; kt += 2) {
-            tile.template operator()<0>(kt);
-            if (kt + 1 < n_tiles) {
-                tile.template operator()<1>(kt + 1);
+        const int n_steps = (n_tiles + kStride - 1) / kStride;
+        for (int i = 0; i < n_steps; i += 2) {
+            tile.template operator()<0>(G + kStride * i);
+            if (i + 1 < n_steps) {
+                tile.template operator()<1>(G + kStride * (i + 1));
             }
         }
-
+    };
+    if constexpr (kSplit) {
+        if (split_g == 0) {
+            pipeline.template operator()<0>();
+        } else {
+            pipeline.template operator()<1>();
+        }
+        // Merge of the halves: half 1 leaves O, m_ref and its lane's l in LDS
+        // (the tile buffers, free after the barrier), half 0 rescales both to
+        // the larger reference and stores. A half that saw no key of a row
+        // (row sum 0) has weight 0.
+        __syncthreads();
+        float* mo[4] = {reinterpret_cast<float*>(sVt0), reinterpret_cast<float*>(sVt1),
+                        reinterpret_cast<float*>(sVt2), reinterpret_cast<float*>(sVt3)};
+        float* ml    = reinterpret_cast<float*>(sK0);   // [256] m_ref, [256] l
+        if (split_g == 1) {
+#pragma unroll
+            for (int db = 0; db < 4; ++db) {
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    mo[db][r * kPThreads + ptid] = o[db][r];
+                }
+            }
+            ml[ptid]             = m_ref;
+            ml[kPThreads + ptid] = l_run;
+        }
+        __syncthreads();
+        if (split_g == 1) {
+            return;
+        }
+        const float m1   = ml[ptid];
+        const float l1   = ml[kPThreads + ptid];
+        const bool  use1 = wave_xor_sum(l1, 32) > 0.0f;
+        const float mm   = use1 ? fmaxf(m_ref, m1) : m_ref;
+        const float f0   = __builtin_amdgcn_exp2f(m_ref - mm);
+        const float f1   = use1 ? __builtin_amdgcn_exp2f(m1 - mm) : 0.0f;
+#pragma unroll
+        for (int db = 0; db < 4; ++db) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                o[db][r] = o[db][r] * f0 + mo[db][r * kPThreads + ptid] * f1;
+            }
+        }
+        l_run = l_run * f0 + l1 * f1;
+    } else {
+        pipeline.template operator()<0>();
+    }
     }
 
     const float l_tot = wave_xor_sum(l_run, 32);
@@ -733,21 +804,22 @@ __global__ __launch_bounds__(kWaves * kWave, 2) void flash_prefill_kernel(
     }
 }
 
-template <int kWaves>
+template <int kWaves, bool kSplit = false>
 void launch_prefill(uint16_t* out, const uint16_t* q, const uint8_t* k, const uint8_t* v,
                     const float* k_scale, const float* v_scale, int n_new, const int* cache_len,
                     int hq, int hkv, float scale_log2, hipStream_t stream,
                     const int* block_table, int block_shift, bool one_round) {
-    const int  n_blk = (n_new + 32 * kWaves - 1) / (32 * kWaves);
-    const dim3 grid(static_cast<unsigned>(n_blk * hq));
+    constexpr int kBM   = 32 * (kSplit ? 4 : kWaves);
+    const int     n_blk = (n_new + kBM - 1) / kBM;
+    const dim3    grid(static_cast<unsigned>(n_blk * hq));
     if (block_table != nullptr) {
-        hipLaunchKernelGGL((flash_prefill_kernel<kWaves, true>), grid, dim3(kWaves * kWave), 0,
-                           stream, out, q, k, v, k_scale, v_scale, n_new, cache_len, hq, hkv,
-                           scale_log2, block_table, block_shift, one_round);
+        hipLaunchKernelGGL((flash_prefill_kernel<kWaves, true, kSplit>), grid,
+                           dim3(kWaves * kWave), 0, stream, out, q, k, v, k_scale, v_scale, n_new,
+                           cache_len, hq, hkv, scale_log2, block_table, block_shift, one_round);
     } else {
-        hipLaunchKernelGGL((flash_prefill_kernel<kWaves, false>), grid, dim3(kWaves * kWave), 0,
-                           stream, out, q, k, v, k_scale, v_scale, n_new, cache_len, hq, hkv,
-                           scale_log2, nullptr, 0, one_round);
+        hipLaunchKernelGGL((flash_prefill_kernel<kWaves, false, kSplit>), grid,
+                           dim3(kWaves * kWave), 0, stream, out, q, k, v, k_scale, v_scale, n_new,
+                           cache_len, hq, hkv, scale_log2, nullptr, 0, one_round);
     }
 }
 
@@ -764,20 +836,29 @@ hipError_t flash_prefill_launch(uint16_t* out, const uint16_t* q,
         return hipErrorInvalidValue;
     }
     // 8-wave workgroups (256 rows, one per compute unit: half the staging
-    // per wave) when the grid takes at least two rounds of them; otherwise
-    // 4-wave workgroups (128 rows, two per compute unit) with heavy/light
+    // per wave) when the grid takes at least two rounds of them. Below that,
+    // a compute unit holds too few waves to hide one tile's dependency chain
+    // (~1.4 us per 64-key tile for a lone wave): grids of up to 1.5 rounds of
+    // 128-row blocks, 4 blocks or more per head, split each block's keys over
+    // two 4-wave halves of one workgroup (heaviest block: half the serial
+    // tiles; 1500 x 24 heads 49 -> 36 us, 2048 x 24 50 us from 60); the rest
+    // take 4-wave workgroups (128 rows, two per compute unit) with heavy/light
     // pairing, which balance the causal work of a single round better.
     int dev = 0, cus = 0;
     if (hipGetDevice(&dev) != hipSuccess ||
         hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) {
         cus = 0;
     }
-    const float sl = scale * kLog2e;
+    const float sl       = scale * kLog2e;
+    const int   n_blk128 = (n_new + 127) / 128;
     if (((n_new + 255) / 256) * num_q_heads >= 2 * cus) {
         launch_prefill<8>(out, q, k, v, k_scale, v_scale, n_new, cache_len, num_q_heads,
                           num_kv_heads, sl, stream, block_table, block_shift, false);
+    } else if (n_blk128 >= 4 && 2 * n_blk128 * num_q_heads <= 3 * cus) {
+        launch_prefill<8, true>(out, q, k, v, k_scale, v_scale, n_new, cache_len, num_q_heads,
+                                num_kv_heads, sl, stream, block_table, block_shift, false);
     } else {
-        const bool one_round = ((n_new + 127) / 128) * num_q_heads <= 2 * cus;
+        const bool one_round = n_blk128 * num_q_heads <= 2 * cus;
         launch_prefill<4>(out, q, k, v, k_scale, v_scale, n_new, cache_len, num_q_heads,
                           num_kv_heads, sl, stream, block_table, block_shift, one_round);
     }

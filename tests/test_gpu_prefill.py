@@ -82,14 +82,15 @@ Q_FACTORS = np.array([0.0, 2.0**-130, 2.0**-121, 2.0**-118, 2.0**-60, 1.0, 2.0**
                      dtype=np.float32)
 
 
-@pytest.mark.parametrize("n", [300, 4100])
+@pytest.mark.parametrize("n", [300, 700, 4100])
 def test_q_rows_of_extreme_magnitude(n):
     """q heads scaled from zero and bf16 subnormals up to 2^6 (scores several
     hundred apart between tiles). Tiny rows must keep a finite q split (their
     weights are near uniform); huge rows overflow P and rebase, and the other
     rows of their wave must not be rebased downwards. n 300 runs the 4-wave
-    workgroup with the full oracle, n 4100 the 8-wave one on sampled rows."""
-    hq, hkv, d = (8, 2, 128) if n == 300 else (32, 8, 128)
+    workgroup and n 700 the key-split one with the full oracle, n 4100 the
+    8-wave one on sampled rows."""
+    hq, hkv, d = (8, 2, 128) if n < 1000 else (32, 8, 128)
     scale = np.float32(1.0 / np.sqrt(d))
     f = np.tile(Q_FACTORS, hq // 8)
     q = O.f32_to_bf16(O.bf16_to_f32(O.normal_bf16((n, hq, d), 41)) * f[None, :, None])
@@ -97,12 +98,30 @@ def test_q_rows_of_extreme_magnitude(n):
     v8, vs = O.quantize_kv_fp8(O.normal_bf16((n * hkv, d), 43), d)
     got = gpu_prefill(q, k8, v8, ks, vs, n, 0, hq, hkv, d, scale)
     assert np.isfinite(O.bf16_to_f32(got)).all()
-    if n == 300:
+    if n < 1000:
         want = O.attention_f32(q, k8, v8, ks, vs, n, 0, hq, hkv, d, scale, NTHREADS)
         mx, mean = O.bf16_err(got, want)
         assert mx <= MAX_ABS and mean <= MEAN_ABS, (mx, mean)
     else:
         check_rows(got, q, k8, v8, ks, vs, 0, sampled_rows(n, 12, n), hq, hkv, d, scale)
+
+
+@pytest.mark.parametrize("n_new,clen,hq,hkv", [
+    (513, 0, 8, 2), (513, 129, 16, 4), (640, 64, 8, 8), (777, 1, 24, 8), (1500, 0, 8, 1),
+])
+def test_key_split_workgroups(n_new, clen, hq, hkv):
+    """Grids of at most 1.5 rounds of 128-row blocks (4 or more per head)
+    split each block's key tiles over two halves of one workgroup (even and
+    odd tiles) and merge their (O, max, sum) at the end. Odd and even tile
+    counts, a cache prefix (the odd half's first tile fully masked for the
+    block's first rows when clen = 1), GQA groups of 1 to 8."""
+    d = 128
+    scale = np.float32(1.0 / np.sqrt(d))
+    q, k8, v8, ks, vs = ref_inputs(n_new, clen, hq, hkv, d)
+    got = gpu_prefill(q, k8, v8, ks, vs, n_new, clen, hq, hkv, d, scale)
+    want = O.attention_f32(q, k8, v8, ks, vs, n_new, clen, hq, hkv, d, scale, NTHREADS)
+    mx, mean = O.bf16_err(got, want)
+    assert mx <= MAX_ABS and mean <= MEAN_ABS, (mx, mean)
 
 
 def rope_qkv(n, hq, hkv, d, theta, llama3, seed):
