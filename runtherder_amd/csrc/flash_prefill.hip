@@ -8,7 +8,9 @@
 // MI355X design:
 //  * Workgroup = one q head x (32 x waves) query rows, 32 rows per wave:
 //    8 waves (256 rows, one workgroup per compute unit) when the grid takes
-//    at least two rounds of those, else 4 waves (128 rows, two per compute
+//    at least two rounds of those, else 128 rows: as two 4-wave halves that
+//    split the block's key tiles (even / odd) and merge in LDS, for grids of
+//    4+ blocks per head up to ~1.5 rounds, or as 4 waves (two per compute
 //    unit, heavy and light row blocks paired when the grid is resident in
 //    one round). Longest (last) row blocks first; the q heads of one kv head
 //    on one XCD so their K/V tiles share an L2.
