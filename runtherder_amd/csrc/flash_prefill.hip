@@ -251,8 +251,8 @@ __global__ __launch_bounds__(kWaves * kWave, kSplit ? 1 : 2) void flash_prefill_
     __shared__ __attribute__((aligned(16))) uint16_t sVt1[kHD * kVPitch];
     __shared__ __attribute__((aligned(16))) float    sKf0[kBN];
     __shared__ __attribute__((aligned(16))) float    sKf1[kBN];
-    __shared__ __attribute__((aligned(16))) uint16_t sVt2[kHD * kVPitch];   // key split only
-    __shared__ __attribute__((aligned(16))) uint16_t sVt3[kHD * kVPitch];   // key split only
+    __shared__ __attribute__((aligned(16))) uint16_t sVt2[kHD * kVPitch];   // not 4-wave
+    __shared__ __attribute__((aligned(16))) uint16_t sVt3[kHD * kVPitch];   // not 4-wave
     __shared__ __attribute__((aligned(16))) float    sKf2[kBN];             // key split only
     __shared__ __attribute__((aligned(16))) float    sKf3[kBN];             // key split only
 
@@ -511,7 +511,7 @@ __global__ __launch_bounds__(kWaves * kWave, kSplit ? 1 : 2) void flash_prefill_
         // and does scores, softmax, P V of tile kt; the late group (waves
         // 4-7) does P V of tile kt - 1 (its P kept in registers across the
         // barrier), scores and softmax of tile kt, then stages V(kt + 1) into
-        // the V^T buffer it has just finished reading.
+        // the fourth V^T buffer of a ring of four.
         const bool late = wave >= kWaves / 2;
         const int  gtid = tid & (kThreads / 2 - 1);   // thread index within the group
 
@@ -542,6 +542,16 @@ __global__ __launch_bounds__(kWaves * kWave, kSplit ? 1 : 2) void flash_prefill_
             else if constexpr (R == 2) return sK2;
             else return sK3;
         };
+        // V^T(kt) lives in buffer kt % 4: during tile kt the early group reads
+        // V^T(kt), the late group reads V^T(kt - 1) and then stages
+        // V^T(kt + 1), so the staging never writes a buffer that another
+        // wave of its group may still be reading.
+        auto vbuf4 = [&]<int R>() -> uint16_t* {
+            if constexpr (R == 0) return sVt0;
+            else if constexpr (R == 1) return sVt1;
+            else if constexpr (R == 2) return sVt2;
+            else return sVt3;
+        };
         if (!late) {
             constexpr int kDmaOps = kKTile / 16 / kGThreads;   // copies issued per tile
             // Rows of the tile two ahead, looked up (paged) one tile before use.
@@ -551,7 +561,7 @@ __global__ __launch_bounds__(kWaves * kWave, kSplit ? 1 : 2) void flash_prefill_
                 const uint8_t* kcur = kbuf4.template operator()<R>();
                 uint8_t*       nk   = kbuf4.template operator()<(R + 2) & 3>();
                 const float*   kfb  = B ? sKf1 : sKf0;
-                const uint16_t* vtb = B ? sVt1 : sVt0;
+                const uint16_t* vtb = vbuf4.template operator()<R>();
                 const TileRows<kPaged> r2 = rn;
                 rn = TileRows<kPaged>((kt + 3) * kBN, total, block_table, block_shift);
                 k_tile_dma<kGThreads>(nk, k, r2, kvh, hkv, gtid);
@@ -580,7 +590,8 @@ __global__ __launch_bounds__(kWaves * kWave, kSplit ? 1 : 2) void flash_prefill_
                 constexpr int  B     = R & 1;
                 const uint8_t* kcur  = kbuf4.template operator()<R>();
                 const float*   kfb   = B ? sKf1 : sKf0;
-                uint16_t*      vprev = B ? sVt0 : sVt1;   // V^T(kt - 1), then V^T(kt + 1)
+                uint16_t*      vprev = vbuf4.template operator()<(R + 3) & 3>();   // V^T(kt - 1)
+                uint16_t*      vnext = vbuf4.template operator()<(R + 1) & 3>();   // V^T(kt + 1)
                 float*         nkf   = B ? sKf0 : sKf1;
                 VRaw<kGReps>&  rawc  = B ? raw1 : raw0;
                 VRaw<kGReps>&  rawn  = B ? raw0 : raw1;
@@ -595,7 +606,7 @@ __global__ __launch_bounds__(kWaves * kWave, kSplit ? 1 : 2) void flash_prefill_
                     qk(kcur, sx);
                     softmax(sx, kfb, kt, pop_keep);
                 }
-                v_tile_stage<kGThreads>(rawn, vprev, nkf, gtid, scale_log2);
+                v_tile_stage<kGThreads>(rawn, vnext, nkf, gtid, scale_log2);
                 lds_barrier();
             };
             for (int kt = 0; kt < n_tiles; kt += 4) {
@@ -606,7 +617,12 @@ __global__ __launch_bounds__(kWaves * kWave, kSplit ? 1 : 2) void flash_prefill_
             }
             // P V of the last tile.
             if (n_tiles - 1 < w_tiles) {
-                pv(((n_tiles - 1) & 1) ? sVt1 : sVt0, pop_keep);
+                switch ((n_tiles - 1) & 3) {
+                    case 0: pv(sVt0, pop_keep); break;
+                    case 1: pv(sVt1, pop_keep); break;
+                    case 2: pv(sVt2, pop_keep); break;
+                    default: pv(sVt3, pop_keep); break;
+                }
             }
         }
     } else {
