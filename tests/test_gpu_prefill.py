@@ -124,6 +124,22 @@ def test_key_split_workgroups(n_new, clen, hq, hkv):
     assert mx <= MAX_ABS and mean <= MEAN_ABS, (mx, mean)
 
 
+@pytest.mark.parametrize("n_new", [384, 385, 1536, 1537])
+def test_workgroup_shape_boundaries(n_new):
+    """32 q heads at the edges of the launch's shape choice: 3 / 4 row
+    blocks of 128 (4-wave / key split) and 12 / 13 blocks (key split at 1.5
+    rounds of 256 compute units / 4-wave). Sampled rows of every block edge
+    against the oracle."""
+    hq, hkv, d, clen = 32, 8, 128, 0
+    scale = np.float32(1.0 / np.sqrt(d))
+    q, k8, v8, ks, vs = ref_inputs(n_new, clen, hq, hkv, d)
+    got = gpu_prefill(q, k8, v8, ks, vs, n_new, clen, hq, hkv, d, scale)
+    edges = sorted({r for b in range(0, n_new, 128) for r in (b, b + 63, b + 64, b + 127)
+                    if r < n_new})
+    rows = sorted(set(edges[::3]) | set(sampled_rows(n_new, 6, n_new)))
+    check_rows(got, q, k8, v8, ks, vs, clen, rows, hq, hkv, d, scale)
+
+
 def rope_qkv(n, hq, hkv, d, theta, llama3, seed):
     q = O.normal_bf16((n, hq, d), seed)
     k = O.normal_bf16((n, hkv, d), seed + 1)
