@@ -6,6 +6,7 @@
 // codes and rth_last_error_string() instead of exiting the process.
 #include <hip/hip_runtime.h>
 
+#include <atomic>
 #include <cstdio>
 #include <cstring>
 #include <string>
@@ -15,7 +16,40 @@
 
 namespace rth {
 bool decode_mfma_supported(int num_q_heads, int num_kv_heads, int head_dim);
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::atomic<int> g_cu_count[kMaxDevices];   // 0 = not queried yet
+}  // namespace
+
+hipError_t device_cu_count(int* cus) {
+    int        dev = 0;
+    hipError_t e   = hipGetDevice(&dev);
+    if (e != hipSuccess) {
+        return e;
+    }
+    if (dev >= 0 && dev < kMaxDevices) {
+        const int c = g_cu_count[dev].load(std::memory_order_relaxed);
+        if (c > 0) {
+            *cus = c;
+            return hipSuccess;
+        }
+    }
+    int c = 0;
+    e     = hipDeviceGetAttribute(&c, hipDeviceAttributeMultiprocessorCount, dev);
+    if (e != hipSuccess) {
+        return e;
+    }
+    if (c < 1) {
+        return hipErrorInvalidDevice;
+    }
+    if (dev >= 0 && dev < kMaxDevices) {
+        g_cu_count[dev].store(c, std::memory_order_relaxed);
+    }
+    *cus = c;
+    return hipSuccess;
 }
+}  // namespace rth
 
 namespace {
 

@@ -19,26 +19,29 @@
 //  * Softmax runs in base 2 (scores pre-multiplied by scale*log2(e)); the
 //    running-max rescale of the accumulator is skipped when no lane's max
 //    moved.
-//  * Two partitions, chosen on device from *cache_len:
-//      - long contexts (> kCoopMaxKeys keys): one WAVE per (kv head, split)
-//        unit, num_splits splits. A workgroup holds the kv heads of one
-//        split (its waves share the interleaved scale lines in L1); waves
-//        never wait for each other and each writes its own partial.
-//      - short contexts: one WORKGROUP per (kv head, split), the eight waves
-//        take alternate tiles and merge in LDS, so 8x fewer partials reach
-//        the merge kernel (whose launch and loads dominate at this size).
-//        Workgroups of one split for all kv heads land on one XCD.
-//  * A second small kernel merges the splits of every (q head, 32-wide d
-//    slice): one round of loads, an online max per thread over a strided
-//    subset of splits, then a tree merge in LDS. The scratch layout is the
-//    reference's ([Hq,S] m, [Hq,S] l, [Hq,S,D] acc); it needs no
-//    initialization.
+//  * Partitions (see DecPartition):
+//      - num_splits * Hkv >= 8 * CUs units, long contexts (> kCoopMaxKeys
+//        keys): one WAVE per (kv head, split) unit. A workgroup holds the kv
+//        heads of one split (its waves share the interleaved scale lines in
+//        L1); waves never wait for each other and each writes its own
+//        partial.
+//      - the same launch at short contexts: one WORKGROUP per (kv head,
+//        split) over 8x fewer splits, the eight waves take alternate tiles
+//        and merge in LDS (the merge kernel's loads dominate at this size).
+//      - fewer units (e.g. 64 splits x 8 kv heads): one workgroup per
+//        (group of kv heads, split), sized so the grid fills the chip; the
+//        waves of one kv head take alternate tiles and merge in LDS.
+//        Workgroups of one split land on one XCD.
+//  * A second small kernel merges the splits of every (q head, 16-wide d
+//    slice): one round of loads issued before *cache_len is known, an
+//    online max per thread over a strided subset of splits, lane exchanges,
+//    one LDS step. The scratch layout is the reference's ([Hq,S] m, [Hq,S]
+//    l, [Hq,S,D] acc); it needs no initialization.
 //
-// The key range of split si is [si*per, min(si*per+per, n_keys)) with
-// per = 32 * ceil(ceil(n_keys / splits) / 32); splits past the last key exit
-// at once and the merge skips them. n_keys = *cache_len + 1 is read on
-// device, so one launch configuration serves every decode step (graph
-// capturable).
+// Split si holds an even share of the kTileKeys-key tiles over the keys; the
+// merge folds the first n_eff = min(splits, tiles) slots. n_keys =
+// *cache_len + 1 is read on device, so one launch configuration serves every
+// decode step (graph capturable).
 #include "device_common.hpp"
 #include "launch.hpp"
 
@@ -49,10 +52,9 @@ constexpr int kDecWaves   = 8;
 constexpr int kDecThreads = kDecWaves * kWave;
 constexpr int kTileKeys   = 32;     // keys per wave iteration (two 16-key MFMAs)
 constexpr int kMaxGroupD  = 2048;   // G * head_dim bound of a wave's LDS partial staging
-constexpr int kCombineThreads = 256;
-constexpr int kCombineSlice   = 32;    // head_dim slice per merge workgroup
+constexpr int kCombineThreads = 128;
+constexpr int kCombineSlice   = 16;    // head_dim slice per merge workgroup
 constexpr int kCoopMaxKeys    = 4096;  // contexts up to this run cooperative workgroups
-constexpr int kWideUnits      = 1024;  // fewer (kv head, split) units: one workgroup each
 constexpr int kNtMinTiles     = 8;     // tiles past the first a wave streams with nontemporal loads
 
 template <int D>
@@ -146,38 +148,76 @@ __device__ __forceinline__ void load_tile(TileRaw<D>& t, const uint8_t* __restri
     }
 }
 
-// Partition of the decode work for one call. With few units
-// (num_splits * hkv < kWideUnits) the host launches one workgroup per
-// (kv head, split) and the eight waves of a workgroup share its key range,
-// merging in LDS ("coop"). Otherwise it launches one wave per unit, eight per
-// workgroup; then long contexts run one wave per (kv head, split) unit
-// (num_splits splits, no merge inside a workgroup) and contexts up to
-// kCoopMaxKeys switch to coop over n_wgs / hkv splits, which leaves 8x fewer
-// partials for the merge kernel. Both kernels derive the same partition from
-// *cache_len and the launch shape, so it is decided on device per call.
+// Partition of the decode work for one call. With fewer units than one
+// round of wave slots (num_splits * hkv < 8 * CUs) the host launches one
+// workgroup per (group of kvg kv heads, split): the workgroup's waves are kvg kv heads x
+// 8 / kvg waves per kv head, the waves of one kv head take alternate tiles of
+// the split and merge in LDS ("coop"); kvg is chosen so the grid still fills
+// the chip (more kv heads per workgroup read longer runs of each interleaved
+// [token, kv_head] row). Otherwise it launches one wave per unit, eight per
+// workgroup (kvg = 0); then long contexts run one wave per (kv head, split)
+// unit (num_splits splits, no merge inside a workgroup) and contexts up to
+// kCoopMaxKeys switch to coop with one kv head per workgroup over n_wgs / hkv
+// splits, which leaves 8x fewer partials for the merge kernel. Both kernels
+// derive the same partition from *cache_len and the launch shape, so it is
+// decided on device per call.
+//
+// The key range is cut into kTileKeys-key tiles dealt out evenly: split si
+// holds tiles [split_tile(si), split_tile(si + 1)), floor or ceil of
+// tiles / n_eff of them, and n_eff = min(splits, tiles) splits are live, the
+// first n_eff slots of the partials (at ctx 8196 and 256 splits: one split
+// of two tiles and 255 of one, where equal 64-key ranges would leave 127
+// splits empty and their workgroups idle).
 struct DecPartition {
     bool coop;
-    int  splits;   // partials per q head
-    int  per;      // keys per split (multiple of kTileKeys)
-    int  n_eff;    // splits holding at least one key
+    int  splits;   // partial slots per q head
+    int  n_eff;    // live splits: min(splits, tiles)
+    int  base;     // tiles / n_eff
+    int  rem;      // tiles % n_eff: the first rem splits hold one more tile
+    int  gkv;      // coop: kv heads per workgroup
 };
 
+__device__ __forceinline__ int split_tile(const DecPartition& pt, int si) {
+    return si * pt.base + min(si, pt.rem);
+}
+
 __device__ __forceinline__ DecPartition dec_partition(int n_keys, int num_splits, int hkv,
-                                                      int n_wgs) {
+                                                      int n_wgs, int kvg) {
     DecPartition pt;
-    const int coop_splits = n_wgs / hkv;
-    const bool wide       = n_wgs >= num_splits * hkv;
-    pt.coop               = wide || ((n_keys <= kCoopMaxKeys) && (coop_splits >= 1));
-    pt.splits             = pt.coop ? coop_splits : num_splits;
-    int per               = (n_keys + pt.splits - 1) / pt.splits;
-    pt.per                = (per + kTileKeys - 1) & ~(kTileKeys - 1);
-    pt.n_eff              = (n_keys + pt.per - 1) / pt.per;
+    if (kvg > 0) {
+        pt.coop   = true;
+        pt.splits = num_splits;
+        pt.gkv    = kvg;
+    } else {
+        const int coop_splits = n_wgs / hkv;
+        pt.coop               = (n_keys <= kCoopMaxKeys) && (coop_splits >= 1);
+        pt.splits             = pt.coop ? coop_splits : num_splits;
+        pt.gkv                = 1;
+    }
+    const int tiles = (n_keys + kTileKeys - 1) / kTileKeys;
+    pt.n_eff        = min(pt.splits, tiles);
+    pt.base         = tiles / pt.n_eff;
+    pt.rem          = tiles - pt.base * pt.n_eff;
     return pt;
 }
 
-__host__ __device__ constexpr int dec_workgroups(int num_splits, int hkv) {
-    return (num_splits * hkv < kWideUnits) ? num_splits * hkv
-                                           : (num_splits * hkv + kDecWaves - 1) / kDecWaves;
+// kv heads per workgroup of a coop launch (0: one wave per unit): the
+// largest of 8, 4, 2, 1 dividing hkv that leaves at least `cus` workgroups.
+__host__ __device__ constexpr int dec_group_kv(int num_splits, int hkv, int cus) {
+    if (num_splits * hkv >= kDecWaves * cus) {
+        return 0;
+    }
+    for (int g = kDecWaves; g > 1; g /= 2) {
+        if (hkv % g == 0 && num_splits * (hkv / g) >= cus) {
+            return g;
+        }
+    }
+    return 1;
+}
+
+__host__ __device__ constexpr int dec_workgroups(int num_splits, int hkv, int kvg) {
+    return (kvg > 0) ? num_splits * (hkv / kvg)
+                     : (num_splits * hkv + kDecWaves - 1) / kDecWaves;
 }
 
 // The appended token's quantized K/V codes for one (kv head) unit, laid out
@@ -290,7 +330,7 @@ __global__ __launch_bounds__(kDecThreads) void flash_decode_kernel(
     const int* __restrict__ cache_len, int hq, int hkv, float scale_log2,
     const uint16_t* __restrict__ k_new, const uint16_t* __restrict__ v_new,
     uint8_t* k_w, uint8_t* v_w, float* ks_w, float* vs_w,
-    const int* __restrict__ block_table, int block_shift) {
+    const int* __restrict__ block_table, int block_shift, int kvg) {
     using T = DecTraits<D>;
 
     __shared__ __attribute__((aligned(16))) float sm_sc[kDecWaves][64];
@@ -308,39 +348,47 @@ __global__ __launch_bounds__(kDecThreads) void flash_decode_kernel(
 
     const int          n_keys = *cache_len + 1;
     const DecPartition pt     = dec_partition(n_keys, num_splits, hkv,
-                                              static_cast<int>(gridDim.x));
-    // coop: workgroup = (kv head, split), waves take tiles wave, wave + 8, ...
+                                              static_cast<int>(gridDim.x), kvg);
+    // coop: workgroup = (group of gkv kv heads, split); wave w serves kv head
+    //       w % gkv of the group and takes tiles w / gkv, + 8 / gkv, ...
     // solo: wave = (kv head, split) unit; adjacent units are the kv heads of
     //       one split, so a workgroup's waves share the scale lines in L1.
-    int kvh, si;
+    int       kvh, si;
+    const int wpk = kDecWaves / pt.gkv;   // coop: waves per kv head
     if (!pt.coop) {
         const int unit = bid * kDecWaves + wave;
         kvh            = unit % hkv;
         si             = unit / hkv;
-    } else if ((pt.splits & 7) == 0) {
-        // All kv heads of one split on one XCD (bid % 8), so the interleaved
-        // [token, kv_head] K/V rows and scale lines are fetched into one L2.
-        const int r = bid >> 3;
-        si          = (r / hkv) * 8 + (bid & 7);
-        kvh         = r % hkv;
     } else {
-        si  = bid / hkv;
-        kvh = bid % hkv;
+        const int groups = hkv / pt.gkv;
+        int       grp;
+        if ((pt.splits & 7) == 0) {
+            // All kv heads of one split on one XCD (bid % 8), so the
+            // interleaved [token, kv_head] K/V rows and scale lines are
+            // fetched into one L2.
+            const int r = bid >> 3;
+            si          = (r / groups) * 8 + (bid & 7);
+            grp         = r % groups;
+        } else {
+            si  = bid / groups;
+            grp = bid % groups;
+        }
+        kvh = grp * pt.gkv + wave % pt.gkv;
     }
     if (si >= pt.n_eff) {   // uniform per workgroup in coop mode
         return;
     }
-    const int k0 = si * pt.per;
+    const int k0 = split_tile(pt, si) * kTileKeys;
     // With an append, the split holding the new key (the last one) reads
     // only the keys before it from the cache; one of its waves adds the new
     // key from registers.
     const int  p_new   = n_keys - 1;
     const bool owner   = kAppend && (si == pt.n_eff - 1);
-    const bool virt    = owner && (!pt.coop || wave == kDecWaves - 1);
-    const int  k1      = owner ? p_new : min(k0 + pt.per, n_keys);
+    const bool virt    = owner && (!pt.coop || wave >= kDecWaves - pt.gkv);
+    const int  k1      = owner ? p_new : min(split_tile(pt, si + 1) * kTileKeys, n_keys);
     const int  n_tiles = (k1 - k0 + kTileKeys - 1) / kTileKeys;
-    const int  t_first = pt.coop ? wave : 0;
-    const int  t_step  = pt.coop ? kDecWaves : 1;
+    const int  t_first = pt.coop ? wave / pt.gkv : 0;
+    const int  t_step  = pt.coop ? wpk : 1;
 
     // Q^T as the B operand: column n = q head of the group (zero past G).
     bf16x8 qop[T::kKSteps];
@@ -505,12 +553,13 @@ __global__ __launch_bounds__(kDecThreads) void flash_decode_kernel(
                 }
             }
         };
-        // A wave that streams many tiles on its own (long splits) is
-        // bandwidth-bound: nontemporal loads. Short splits and cooperative
+        // A wave that streams many tiles (long splits) is bandwidth-bound:
+        // nontemporal loads. Short runs and the one-kv-head cooperative
         // workgroups are latency-bound: plain loads (measured: 128K at 256
         // splits 56.3 -> 51.8 us with nontemporal loads; 8K at 256 splits
-        // and 128K at 64 cooperative splits 6-8 % slower with them).
-        if (!pt.coop && last_tile - t_first >= kNtMinTiles) {
+        // and 128K at 64 one-kv-head cooperative splits 6-8 % slower with
+        // them; 128K at 64 splits in two-kv-head workgroups 0.5 us faster).
+        if ((!pt.coop || pt.gkv > 1) && last_tile - t_first >= kNtMinTiles) {
             stream.template operator()<true>();
         } else {
             stream.template operator()<false>();
@@ -537,18 +586,24 @@ __global__ __launch_bounds__(kDecThreads) void flash_decode_kernel(
     float*        part_l = partial + hs;
     float*        part_o = partial + 2 * hs;
     if (pt.coop) {
-        // Merge the eight waves: each scales its O^T by 2^(m_w - M) into its
-        // LDS rows, then the rows are summed along d.
+        // Merge the waves of each kv head (waves kl, kl + gkv, ...): each
+        // scales its O^T by 2^(m_w - M) into its LDS rows, then the rows are
+        // summed along d.
         if (g == 0) {
             sm_m[wave][n] = m_run;
             sm_l[wave][n] = l_run;
         }
         __syncthreads();
+        // Loops over the waves of one kv head run over all kDecWaves slots
+        // with a predicate, unrolled, so their LDS reads issue together.
+        const int kl = wave % pt.gkv;
         if (n < G) {
             float M = -INFINITY;
 #pragma unroll
-            for (int w = 0; w < kDecWaves; ++w) {
-                M = fmaxf(M, sm_m[w][n]);
+            for (int j = 0; j < kDecWaves; ++j) {
+                if (j < wpk) {
+                    M = fmaxf(M, sm_m[kl + j * pt.gkv][n]);
+                }
             }
             const float wf = (m_run == -INFINITY) ? 0.0f : exp2f(m_run - M);
 #pragma unroll
@@ -560,28 +615,41 @@ __global__ __launch_bounds__(kDecThreads) void flash_decode_kernel(
             }
         }
         __syncthreads();
-        for (int e = tid; e < G * (D / 4); e += kDecThreads) {
-            const int h  = e / (D / 4);
-            const int d0 = 4 * (e - h * (D / 4));
+        const int kvh0 = kvh - kl;   // first kv head of the workgroup's group
+        for (int e = tid; e < pt.gkv * G * (D / 4); e += kDecThreads) {
+            const int hg = e / (D / 4);   // (kv head of the group, q head) pair
+            const int el = hg % pt.gkv;
+            const int h  = hg / pt.gkv;
+            const int d0 = 4 * (e - hg * (D / 4));
             f32x4     a  = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int w = 0; w < kDecWaves; ++w) {
-                a += *reinterpret_cast<const f32x4*>(&sm_o[w][h * D + d0]);
+            for (int j = 0; j < kDecWaves; ++j) {
+                if (j < wpk) {
+                    a += *reinterpret_cast<const f32x4*>(&sm_o[el + j * pt.gkv][h * D + d0]);
+                }
             }
-            const int64_t slot = static_cast<int64_t>(kvh * G + h) * num_splits + si;
+            const int64_t slot = static_cast<int64_t>((kvh0 + el) * G + h) * num_splits + si;
             *reinterpret_cast<f32x4*>(&part_o[slot * D + d0]) = a;
         }
-        if (tid < G) {
-            float M = -INFINITY;
-            for (int w = 0; w < kDecWaves; ++w) {
-                M = fmaxf(M, sm_m[w][tid]);
+        if (tid < pt.gkv * G) {
+            const int el = tid % pt.gkv;
+            const int h  = tid / pt.gkv;
+            float     M  = -INFINITY;
+#pragma unroll
+            for (int j = 0; j < kDecWaves; ++j) {
+                if (j < wpk) {
+                    M = fmaxf(M, sm_m[el + j * pt.gkv][h]);
+                }
             }
             float L = 0.0f;
-            for (int w = 0; w < kDecWaves; ++w) {
-                const float mw = sm_m[w][tid];
-                L += (mw == -INFINITY) ? 0.0f : sm_l[w][tid] * exp2f(mw - M);
+#pragma unroll
+            for (int j = 0; j < kDecWaves; ++j) {
+                if (j < wpk) {
+                    const float mw = sm_m[el + j * pt.gkv][h];
+                    L += (mw == -INFINITY) ? 0.0f : sm_l[el + j * pt.gkv][h] * exp2f(mw - M);
+                }
             }
-            const int64_t slot = static_cast<int64_t>(kvh * G + tid) * num_splits + si;
+            const int64_t slot = static_cast<int64_t>((kvh0 + el) * G + h) * num_splits + si;
             part_m[slot]       = M;
             part_l[slot]       = L;
         }
@@ -613,97 +681,121 @@ __global__ __launch_bounds__(kDecThreads) void flash_decode_kernel(
     }
 }
 
-// One workgroup per (q head, 32-wide slice of head_dim): merges the n_eff
+// One workgroup per (q head, 16-wide slice of head_dim): merges the n_eff
 // split partials, out = sum_s 2^(m_s - M) acc_s / sum_s 2^(m_s - M) l_s
 // (reference src/kernels/flash_decode.cu:222-247). Thread (group grp, quad
 // qd) folds splits grp, grp + kGroups, ... for d = 4qd .. 4qd+3 of the slice
-// with an online max, eight loads in flight at a time; the kGroups states
-// merge through LDS.
+// with an online max, eight loads in flight at a time. Its first eight loads
+// are issued before the split count is known (slot indices clamped into the
+// scratch), so they share one round trip with the read of *cache_len; slots
+// no split wrote in this call are dropped by a select. The group states
+// then merge by lane exchanges inside each wave and once through LDS.
 template <int D>
 __global__ __launch_bounds__(kCombineThreads) void flash_decode_combine_kernel(
     uint16_t* __restrict__ out, const float* __restrict__ partial, int num_splits,
-    const int* __restrict__ cache_len, int hq, int hkv, int n_wgs) {
+    const int* __restrict__ cache_len, int hq, int hkv, int n_wgs, int kvg) {
     constexpr int kQuads  = kCombineSlice / 4;
     constexpr int kGroups = kCombineThreads / kQuads;
-    __shared__ __attribute__((aligned(16))) f32x4 sm_acc[kGroups][kQuads];
-    __shared__ float sm_mm[kGroups], sm_ll[kGroups];
+    constexpr int kCWaves = kCombineThreads / kWave;
+    static_assert((kQuads & (kQuads - 1)) == 0 && kQuads <= kWave, "lane = kQuads * group + quad");
+    __shared__ __attribute__((aligned(16))) f32x4 sm_acc[kCWaves][kQuads];
+    __shared__ float sm_mm[kCWaves], sm_ll[kCWaves];
 
-    const int qh  = static_cast<int>(blockIdx.x);
-    const int dsl = static_cast<int>(blockIdx.y) * kCombineSlice;
-    const int tid = static_cast<int>(threadIdx.x);
-    const int grp = tid / kQuads;
-    const int qd  = tid - grp * kQuads;
-
-    const int n_keys = *cache_len + 1;
-    const int n_eff  = dec_partition(n_keys, num_splits, hkv, n_wgs).n_eff;
+    const int qh   = static_cast<int>(blockIdx.x);
+    const int dsl  = static_cast<int>(blockIdx.y) * kCombineSlice;
+    const int tid  = static_cast<int>(threadIdx.x);
+    const int grp  = tid / kQuads;
+    const int qd   = tid - grp * kQuads;
+    const int wave = tid / kWave;
+    const int lane = tid & (kWave - 1);
 
     const int64_t hs     = static_cast<int64_t>(hq) * num_splits;
     const float*  part_m = partial + static_cast<int64_t>(qh) * num_splits;
     const float*  part_l = partial + hs + static_cast<int64_t>(qh) * num_splits;
     const float*  part_o = partial + 2 * hs + static_cast<int64_t>(qh) * num_splits * D + dsl;
 
-    float m = -INFINITY, l = 0.0f;
-    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-    for (int s0 = grp; s0 < n_eff; s0 += 8 * kGroups) {
-        float ms[8], ls[8];
-        f32x4 os[8];
+    float ms[8], ls[8];
+    f32x4 os[8];
+    // Unconditional loads of slots s0 + u * kGroups, clamped to slot `cap`.
+    auto load8 = [&](int s0, int cap) {
 #pragma unroll
         for (int u = 0; u < 8; ++u) {
-            const int s = s0 + u * kGroups;
-            ms[u]       = -INFINITY;
-            ls[u]       = 0.0f;
-            os[u]       = f32x4{0.f, 0.f, 0.f, 0.f};
-            if (s < n_eff) {
-                ms[u] = part_m[s];
-                ls[u] = part_l[s];
-                os[u] = *reinterpret_cast<const f32x4*>(&part_o[static_cast<int64_t>(s) * D + 4 * qd]);
-            }
+            const int s = min(s0 + u * kGroups, cap);
+            ms[u]       = part_m[s];
+            ls[u]       = part_l[s];
+            os[u]       = *reinterpret_cast<const f32x4*>(&part_o[static_cast<int64_t>(s) * D + 4 * qd]);
         }
+    };
+    float m = -INFINITY, l = 0.0f;
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    // Folds the loaded slots below n_eff; the others may hold anything (NaN
+    // included), so they are selected away, never multiplied by zero.
+    auto fold = [&](int s0, int n_eff) {
+        float mv[8];
         float mx = m;
 #pragma unroll
         for (int u = 0; u < 8; ++u) {
-            mx = fmaxf(mx, ms[u]);
+            mv[u] = (s0 + u * kGroups < n_eff) ? ms[u] : -INFINITY;
+            mx    = fmaxf(mx, mv[u]);
         }
         const float c = (m == -INFINITY) ? 0.0f : exp2f(m - mx);
         acc *= c;
         l *= c;
 #pragma unroll
         for (int u = 0; u < 8; ++u) {
-            const float f = (ms[u] == -INFINITY) ? 0.0f : exp2f(ms[u] - mx);
-            acc += os[u] * f;
-            l += ls[u] * f;
+            const bool  live = mv[u] != -INFINITY;
+            const float f    = live ? exp2f(mv[u] - mx) : 0.0f;
+            const f32x4 o    = live ? os[u] : f32x4{0.f, 0.f, 0.f, 0.f};
+            acc += o * f;
+            l += (live ? ls[u] : 0.0f) * f;
         }
         m = mx;
+    };
+    load8(grp, num_splits - 1);
+    const int n_keys = *cache_len + 1;
+    const int n_eff  = dec_partition(n_keys, num_splits, hkv, n_wgs, kvg).n_eff;
+    fold(grp, n_eff);
+    for (int s0 = grp + 8 * kGroups; s0 < n_eff; s0 += 8 * kGroups) {
+        load8(s0, n_eff - 1);
+        fold(s0, n_eff);
     }
-    // Tree merge of the kGroups states: at each level the upper half of the
-    // groups hands its state to the lower half through LDS.
+
+    auto merge = [&](float m2, float l2, f32x4 a2) {
+        const float M  = fmaxf(m, m2);
+        const float f1 = (m == -INFINITY) ? 0.0f : exp2f(m - M);
+        const float f2 = (m2 == -INFINITY) ? 0.0f : exp2f(m2 - M);
+        acc            = acc * f1 + a2 * f2;
+        l              = l * f1 + l2 * f2;
+        m              = M;
+    };
+    // The groups of a wave differ in the lane bits above the quad index.
 #pragma unroll
-    for (int stride = kGroups / 2; stride >= 1; stride /= 2) {
-        if (grp >= stride && grp < 2 * stride) {
-            sm_acc[grp - stride][qd] = acc;
-            if (qd == 0) {
-                sm_mm[grp - stride] = m;
-                sm_ll[grp - stride] = l;
-            }
+    for (int mask = kQuads; mask < kWave; mask <<= 1) {
+        f32x4 a2;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            a2[e] = __shfl_xor(acc[e], mask);
         }
-        __syncthreads();
-        if (grp < stride) {
-            const float m2 = sm_mm[grp];
-            const float M  = fmaxf(m, m2);
-            const float f1 = (m == -INFINITY) ? 0.0f : exp2f(m - M);
-            const float f2 = (m2 == -INFINITY) ? 0.0f : exp2f(m2 - M);
-            acc            = acc * f1 + sm_acc[grp][qd] * f2;
-            l              = l * f1 + sm_ll[grp] * f2;
-            m              = M;
-        }
-        __syncthreads();
+        merge(__shfl_xor(m, mask), __shfl_xor(l, mask), a2);
     }
-    if (grp == 0) {
+    if (lane < kQuads) {
+        sm_acc[wave][lane] = acc;
+        if (lane == 0) {
+            sm_mm[wave] = m;
+            sm_ll[wave] = l;
+        }
+    }
+    __syncthreads();
+    if (wave == 0 && lane < kQuads) {
+#pragma unroll
+        for (int w = 1; w < kCWaves; ++w) {
+            merge(sm_mm[w], sm_ll[w], sm_acc[w][lane]);
+        }
         const float inv = 1.0f / l;
         u32x2       w2;
         w2.x = pack_bf16x2(acc[0] * inv, acc[1] * inv);
         w2.y = pack_bf16x2(acc[2] * inv, acc[3] * inv);
-        *reinterpret_cast<u32x2*>(out + static_cast<int64_t>(qh) * D + dsl + 4 * qd) = w2;
+        *reinterpret_cast<u32x2*>(out + static_cast<int64_t>(qh) * D + dsl + 4 * lane) = w2;
     }
 }
 
@@ -721,18 +813,24 @@ hipError_t launch_decode(uint16_t* out, const uint16_t* q, const uint8_t* k,
                          const uint16_t* v_new, uint8_t* k_w, uint8_t* v_w, float* ks_w,
                          float* vs_w, const int* block_table, int block_shift,
                          hipStream_t stream) {
-    const int  n_wgs = dec_workgroups(num_splits, hkv);
+    int        cus = 0;
+    hipError_t ce  = device_cu_count(&cus);
+    if (ce != hipSuccess) {
+        return ce;
+    }
+    const int  kvg   = dec_group_kv(num_splits, hkv, cus);
+    const int  n_wgs = dec_workgroups(num_splits, hkv, kvg);
     const dim3 grid(static_cast<unsigned>(n_wgs));
     if (k_new != nullptr) {
         hipLaunchKernelGGL((flash_decode_kernel<D, true, kPaged>), grid, dim3(kDecThreads), 0,
                            stream, q, k, v, ks, vs, partial, num_splits, cache_len, hq, hkv,
                            scale * kLog2e, k_new, v_new, k_w, v_w, ks_w, vs_w, block_table,
-                           block_shift);
+                           block_shift, kvg);
     } else {
         hipLaunchKernelGGL((flash_decode_kernel<D, false, kPaged>), grid, dim3(kDecThreads), 0,
                            stream, q, k, v, ks, vs, partial, num_splits, cache_len, hq, hkv,
                            scale * kLog2e, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr,
-                           block_table, block_shift);
+                           block_table, block_shift, kvg);
     }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) {
@@ -741,7 +839,7 @@ hipError_t launch_decode(uint16_t* out, const uint16_t* q, const uint8_t* k,
     hipLaunchKernelGGL(flash_decode_combine_kernel<D>,
                        dim3(static_cast<unsigned>(hq), static_cast<unsigned>(D / kCombineSlice)),
                        dim3(kCombineThreads), 0, stream, out, partial, num_splits,
-                       cache_len, hq, hkv, n_wgs);
+                       cache_len, hq, hkv, n_wgs, kvg);
     return hipGetLastError();
 }
 

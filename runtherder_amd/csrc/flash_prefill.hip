@@ -768,6 +768,12 @@ __global__ __launch_bounds__(kWaves * kWave, kSplit ? 1 : 2) void flash_prefill_
         // the larger reference and stores. A half that saw no key of a row
         // (row sum 0) has weight 0.
         __syncthreads();
+        // The merge reuses the tile buffers: each V^T buffer holds one d block
+        // of O (16 floats per thread), sK0 holds m_ref and l of every thread.
+        static_assert(kHD * kVPitch * sizeof(uint16_t) >= 16 * kPThreads * sizeof(float),
+                      "a V^T buffer must hold a d block of O for every thread");
+        static_assert(kKTile >= 2 * kPThreads * sizeof(float),
+                      "a K buffer must hold m_ref and l for every thread");
         float* mo[4] = {reinterpret_cast<float*>(sVt0), reinterpret_cast<float*>(sVt1),
                         reinterpret_cast<float*>(sVt2), reinterpret_cast<float*>(sVt3)};
         float* ml    = reinterpret_cast<float*>(sK0);   // [256] m_ref, [256] l
@@ -862,10 +868,10 @@ hipError_t flash_prefill_launch(uint16_t* out, const uint16_t* q,
     // tiles; 1500 x 24 heads 49 -> 36 us, 2048 x 24 50 us from 60); the rest
     // take 4-wave workgroups (128 rows, two per compute unit) with heavy/light
     // pairing, which balance the causal work of a single round better.
-    int dev = 0, cus = 0;
-    if (hipGetDevice(&dev) != hipSuccess ||
-        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) {
-        cus = 0;
+    int        cus = 0;
+    hipError_t ce  = device_cu_count(&cus);
+    if (ce != hipSuccess) {
+        return ce;
     }
     const float sl       = scale * kLog2e;
     const int   n_blk128 = (n_new + 127) / 128;

@@ -10,6 +10,10 @@
 
 namespace rth {
 
+// Compute units of the current device, queried once per device and cached;
+// returns the query's error (and leaves *cus unchanged) if it fails.
+hipError_t device_cu_count(int* cus);
+
 hipError_t quantize_kv_fp8_launch(uint8_t* q, float* scale, const uint16_t* x,
                                   const int* at_pos, int rows_per_pos,
                                   int num_rows, int head_dim, hipStream_t stream);

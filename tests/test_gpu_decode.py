@@ -153,6 +153,24 @@ def test_long_splits_ragged_tail():
     check(got, q, k8, v8, ks, vs, ctx - 1, hq, hkv, d, scale)
 
 
+@pytest.mark.parametrize("ctx,hq,hkv,splits", [
+    (20000, 32, 8, 64), (20001, 32, 8, 128), (7000, 32, 8, 16), (12345, 16, 4, 128),
+    (3000, 32, 8, 128), (33, 32, 8, 64),
+])
+def test_grouped_workgroups(ctx, hq, hkv, splits):
+    """Launches with fewer (kv head, split) units than one round of wave
+    slots run one workgroup per (group of kv heads, split), the waves of a kv
+    head on alternate tiles, merged in LDS. On 256 compute units: 64 splits x
+    8 kv heads -> 2 kv heads per workgroup, 128 x 8 -> 4, 16 x 8 -> 1,
+    128 x 4 -> 2; short contexts leave most splits empty."""
+    d = 128
+    scale = np.float32(1.0 / np.sqrt(d))
+    q = O.normal_bf16((hq, d), 81)
+    _, _, k8, v8, ks, vs = make_cache(ctx, hkv, d, kind="normal", seed=ctx)
+    got = gpu_decode(q, k8, v8, ks, vs, ctx - 1, hq, hkv, d, splits, scale)
+    check(got, q, k8, v8, ks, vs, ctx - 1, hq, hkv, d, scale)
+
+
 def test_repeated_calls_share_scratch():
     """Back-to-back calls with different depths on one scratch stay correct
     (the scratch carries no state between calls)."""
@@ -194,6 +212,7 @@ def test_score_dynamic_range(splits):
     (0, 24, 8, 128, None), (1, 24, 8, 128, None), (31, 24, 8, 128, None), (32, 24, 8, 128, None),
     (2040, 24, 8, 128, None), (8195, 24, 8, 128, None), (9000, 32, 8, 128, 64),
     (130, 8, 2, 64, 8), (700, 8, 4, 256, 16), (77, 64, 4, 128, 4), (40, 8, 2, 32, 4),
+    (5000, 32, 8, 128, 128), (6000, 16, 4, 128, 128),
 ])
 def test_decode_append_fused(cache_len, hq, hkv, d, splits):
     """Fused append + decode: the cache row equals the append kernel's bytes

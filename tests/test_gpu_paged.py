@@ -1,17 +1,22 @@
 """Paged KV layout (no reference counterpart; the reference README plans paged
-attention, README.md:142-143): a paged cache with a shuffled block table must
-hold, after gathering, the bytes the contiguous cache holds, and decode /
-fused append+decode / prefill over it must return exactly the contiguous
-results (same data, same order of work)."""
+attention, README.md:142-143). The oracle is the reference's own math on the
+GATHERED cache: the paged slabs, read back through the block table, must hold
+the bytes the oracle's quantizer (quantization.cu:200-254) produces, and
+decode / fused append+decode / prefill over the paged cache must match the
+oracle's attention (attention.cu:34-91) on those gathered bytes within
+max-abs 2e-2 / mean-abs 2e-3. Each case also checks that the paged result is
+bit-identical to the contiguous cache's (same data, same order of work)."""
 import numpy as np
 import pytest
 import torch
 
 import oracle_lib as O
 import runtherder_amd as R
-from gpu_util import DEV, bf16_dev, bf16_host, i32_dev, int_dev, step, sync
+from gpu_util import DEV, NTHREADS, bf16_dev, bf16_host, i32_dev, int_dev, step, sync
 
 pytestmark = pytest.mark.gpu
+
+MAX_ABS, MEAN_ABS = 2e-2, 2e-3
 
 
 def make_pair(total, hq, hkv, d, block, seed):
@@ -36,20 +41,41 @@ def make_pair(total, hq, hkv, d, block, seed):
         paged.append(0, kd, vd, n, int_dev(s0), bt)
         s0 += n
     sync()
-    return cont, paged, bt, table
+    return cont, paged, bt, table, k, v
 
 
 def gather(paged, table, total, block):
+    """Logical rows 0..total-1 of the paged slabs, read through the block table
+    on the host (independent of the kernels' address arithmetic)."""
     rows = np.concatenate([np.arange(b * block, (b + 1) * block) for b in table])[:total]
     return (paged.k[0].cpu().numpy()[rows], paged.v[0].cpu().numpy()[rows],
             paged.k_scale[0].cpu().numpy()[rows], paged.v_scale[0].cpu().numpy()[rows])
 
 
+def assert_bytes_match_oracle(gk, gv, gks, gvs, k, v, d):
+    """Gathered cache == the oracle's quantizer on the bf16 rows, bit for bit."""
+    total, hkv = k.shape[0], k.shape[1]
+    ok, oks = O.quantize_kv_fp8(k, d)
+    ov, ovs = O.quantize_kv_fp8(v, d)
+    assert np.array_equal(gk.reshape(total * hkv, d), ok)
+    assert np.array_equal(gv.reshape(total * hkv, d), ov)
+    assert np.array_equal(gks.reshape(-1).view(np.uint32), oks.view(np.uint32))
+    assert np.array_equal(gvs.reshape(-1).view(np.uint32), ovs.view(np.uint32))
+
+
+def assert_attention_matches_oracle(got, q, gk, gv, gks, gvs, n_new, clen, hq, hkv, d):
+    scale = np.float32(1.0 / np.sqrt(d))
+    want = O.attention_f32(q, gk, gv, gks, gvs, n_new, clen, hq, hkv, d, scale, NTHREADS)
+    mx, mean = O.bf16_err(got.reshape(want.shape), want)
+    assert mx <= MAX_ABS and mean <= MEAN_ABS, (mx, mean)
+
+
 @pytest.mark.parametrize("total,block", [(1500, 64), (3000, 32), (777, 256)])
 def test_paged_append_bytes(total, block):
     hkv, d = 8, 128
-    cont, paged, _, table = make_pair(total, 32, hkv, d, block, total)
+    cont, paged, _, table, k, v = make_pair(total, 32, hkv, d, block, total)
     gk, gv, gks, gvs = gather(paged, table, total, block)
+    assert_bytes_match_oracle(gk, gv, gks, gvs, k, v, d)
     assert np.array_equal(gk, cont.k[0].cpu().numpy()[:total])
     assert np.array_equal(gv, cont.v[0].cpu().numpy()[:total])
     assert np.array_equal(gks.view(np.uint32), cont.k_scale[0].cpu().numpy()[:total].view(np.uint32))
@@ -60,52 +86,71 @@ def test_paged_append_bytes(total, block):
                                                 (5000, 32, 64), (300, 64, 7)])
 def test_paged_decode_equals_contiguous(total, block, splits):
     hq, hkv, d = 24, 8, 128
-    cont, paged, bt, _ = make_pair(total, hq, hkv, d, block, 10 + total)
+    cont, paged, bt, table, _, _ = make_pair(total, hq, hkv, d, block, 10 + total)
     cfg = R.AttnConfig.for_heads(hq, hkv, d)
     be = R.AdaptiveAttention(cfg, splits)
-    q = bf16_dev(O.normal_bf16((hq, d), 20 + total))
+    qh = O.normal_bf16((hq, d), 20 + total)
+    q = bf16_dev(qh)
     o1 = torch.empty((hq, d), dtype=torch.bfloat16, device=DEV)
     o2 = torch.empty_like(o1)
     step(f"paged decode total={total} block={block} splits={be.num_splits}")
     be.run(o1, q, cont.view(0), 1, int_dev(total - 1))
     be.run(o2, q, paged.view(0, bt), 1, int_dev(total - 1))
     sync()
-    assert np.array_equal(bf16_host(o1), bf16_host(o2))
+    got = bf16_host(o2)
+    assert_attention_matches_oracle(got, qh, *gather(paged, table, total, block), 1, total - 1,
+                                    hq, hkv, d)
+    assert np.array_equal(bf16_host(o1), got)
 
 
 @pytest.mark.parametrize("total,block", [(2041, 64), (9000, 32)])
 def test_paged_fused_append_decode_equals_contiguous(total, block):
     hq, hkv, d = 24, 8, 128
-    cont, paged, bt, table = make_pair(total - 1, hq, hkv, d, block, 30 + total)
+    cont, paged, bt, table, k, v = make_pair(total - 1, hq, hkv, d, block, 30 + total)
     cfg = R.AttnConfig.for_heads(hq, hkv, d)
     be = R.AdaptiveAttention(cfg)
-    q = bf16_dev(O.normal_bf16((hq, d), 40 + total))
-    kn = bf16_dev(O.normal_bf16((hkv, d), 41))
-    vn = bf16_dev(O.normal_bf16((hkv, d), 42))
+    qh = O.normal_bf16((hq, d), 40 + total)
+    q = bf16_dev(qh)
+    knh = O.normal_bf16((hkv, d), 41)
+    vnh = O.normal_bf16((hkv, d), 42)
+    kn, vn = bf16_dev(knh), bf16_dev(vnh)
     o1 = torch.empty((hq, d), dtype=torch.bfloat16, device=DEV)
     o2 = torch.empty_like(o1)
     step(f"paged fused append+decode total={total} block={block}")
     be.run_decode_append(o1, q, cont.view(0), kn, vn, int_dev(total - 1))
     be.run_decode_append(o2, q, paged.view(0, bt), kn, vn, int_dev(total - 1))
     sync()
-    assert np.array_equal(bf16_host(o1), bf16_host(o2))
-    gk, _, gks, _ = gather(paged, table, total, block)
+    got = bf16_host(o2)
+    assert np.array_equal(bf16_host(o1), got)
+    gk, gv, gks, gvs = gather(paged, table, total, block)
+    # The appended token's row is the oracle quantizer's, like every earlier row.
+    assert_bytes_match_oracle(gk, gv, gks, gvs, np.concatenate([k, knh[None]]),
+                              np.concatenate([v, vnh[None]]), d)
     assert np.array_equal(gk, cont.k[0].cpu().numpy()[:total])
     assert np.array_equal(gks.view(np.uint32), cont.k_scale[0].cpu().numpy()[:total].view(np.uint32))
+    assert_attention_matches_oracle(got, qh, gk, gv, gks, gvs, 1, total - 1, hq, hkv, d)
 
 
-@pytest.mark.parametrize("total,clen,block", [(1021, 0, 64), (3000, 2237, 32), (4096, 0, 128)])
+# Workgroup shapes on 256 compute units: 1021 and 3000 @ 2237 take the
+# key-split kernel, 200 (two 128-row blocks per head, whole grid resident) the
+# 4-wave kernel with heavy/light pairing, 4096 the 8-wave kernel.
+@pytest.mark.parametrize("total,clen,block", [(1021, 0, 64), (3000, 2237, 32), (4096, 0, 128),
+                                              (200, 0, 32), (1300, 1100, 64)])
 def test_paged_prefill_equals_contiguous(total, clen, block):
     hq, hkv, d = 32, 8, 128
-    cont, paged, bt, _ = make_pair(total, hq, hkv, d, block, 50 + total)
+    cont, paged, bt, table, _, _ = make_pair(total, hq, hkv, d, block, 50 + total)
     cfg = R.AttnConfig.for_heads(hq, hkv, d)
     be = R.AdaptiveAttention(cfg)
     n = total - clen
-    q = bf16_dev(O.normal_bf16((n, hq, d), 60 + total))
+    qh = O.normal_bf16((n, hq, d), 60 + total)
+    q = bf16_dev(qh)
     o1 = torch.empty((n, hq, d), dtype=torch.bfloat16, device=DEV)
     o2 = torch.empty_like(o1)
     step(f"paged prefill total={total} clen={clen} block={block}")
     be.run(o1, q, cont.view(0), n, int_dev(clen))
     be.run(o2, q, paged.view(0, bt), n, int_dev(clen))
     sync()
-    assert np.array_equal(bf16_host(o1), bf16_host(o2))
+    got = bf16_host(o2)
+    assert_attention_matches_oracle(got, qh, *gather(paged, table, total, block), n, clen,
+                                    hq, hkv, d)
+    assert np.array_equal(bf16_host(o1), got)

@@ -124,13 +124,34 @@ def test_key_split_workgroups(n_new, clen, hq, hkv):
     assert mx <= MAX_ABS and mean <= MEAN_ABS, (mx, mean)
 
 
-@pytest.mark.parametrize("n_new", [384, 385, 1536, 1537])
-def test_workgroup_shape_boundaries(n_new):
-    """32 q heads at the edges of the launch's shape choice: 3 / 4 row
-    blocks of 128 (4-wave / key split) and 12 / 13 blocks (key split at 1.5
-    rounds of 256 compute units / 4-wave). Sampled rows of every block edge
-    against the oracle."""
+def shape_boundaries(cus, hq):
+    """Row counts at the edges of flash_prefill_launch's workgroup-shape choice
+    on a device with `cus` compute units (the same formulas as the launcher):
+    the last 4-wave / first key-split count (4 blocks of 128 rows), the last
+    key-split / first 4-wave count (2 * blocks * hq <= 3 * cus), and the first
+    8-wave count (ceil(n / 256) * hq >= 2 * cus)."""
+    out = [384, 385]
+    nb = (3 * cus) // (2 * hq)            # most 128-row blocks on the key split
+    if nb >= 4:
+        out += [128 * nb, 128 * nb + 1]
+    n8 = 256 * (-(-2 * cus // hq) - 1)     # last row count below the 8-wave path
+    out += [n8, n8 + 1]
+    return out
+
+
+@pytest.mark.parametrize("edge", range(6))
+def test_workgroup_shape_boundaries(edge):
+    """32 q heads at the edges of the launch's shape choice, derived from the
+    device's compute-unit count (on 256 CUs: 384 / 385 rows = 3 / 4 blocks of
+    128, 4-wave / key split; 1536 / 1537 = 12 / 13 blocks, key split / 4-wave;
+    3840 / 3841 = 15 / 16 blocks of 256, 4-wave / 8-wave). Sampled rows of
+    every block edge against the oracle."""
     hq, hkv, d, clen = 32, 8, 128, 0
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    edges_n = shape_boundaries(cus, hq)
+    if edge >= len(edges_n):
+        pytest.skip(f"{cus} compute units leave no key-split range for {hq} heads")
+    n_new = edges_n[edge]
     scale = np.float32(1.0 / np.sqrt(d))
     q, k8, v8, ks, vs = ref_inputs(n_new, clen, hq, hkv, d)
     got = gpu_prefill(q, k8, v8, ks, vs, n_new, clen, hq, hkv, d, scale)
