@@ -90,6 +90,23 @@ int rth_attn_decode_split(uint16_t* out, const uint16_t* q, const uint8_t* k,
                           int num_kv_heads, int head_dim, float scale,
                           void* stream);
 
+/* No counterpart in the reference: rth_attn_decode_split without the
+ * `partial` argument, for callers that cannot allocate (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc). It calls no
+ * hipMalloc/hipFree and no allocating library routine: the split partials
+ * live in a fixed 16 MiB device array (2^22 floats) that each GPU holds from
+ * the library's load until the process ends. Rejects shapes with
+ * num_q_heads * num_splits * (head_dim + 2) > 2^22 floats
+ * (RTH_ERR_INVALID_ARG). Every call on one GPU shares that GPU's array:
+ * calls that overlap on one GPU (several streams or host threads) race and
+ * must be serialized by the caller. Output is bit-identical to
+ * rth_attn_decode_split with the same arguments. */
+int rth_attn_decode_split_noalloc(uint16_t* out, const uint16_t* q, const uint8_t* k,
+                                  const uint8_t* v, const float* k_scale,
+                                  const float* v_scale, int num_splits,
+                                  const int* cache_len, int num_q_heads, int num_kv_heads,
+                                  int head_dim, float scale, void* stream);
+
 /* No counterpart in the reference: KVCache::append(layer, k_new, v_new, 1,
  * cache_len) followed by the decode call (reference
  * src/model/supported/llama/llama3.cu:232-234 with n_new == 1) in one call

@@ -21,6 +21,7 @@ from .ops import (  # noqa: F401
     default_num_splits,
     flash_decode_append_split_bf16,
     flash_decode_split_bf16,
+    flash_decode_split_bf16_noalloc,
     flash_prefill_bf16,
     flash_split_scratch_floats,
     make_attention_backend,

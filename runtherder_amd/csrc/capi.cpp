@@ -227,6 +227,43 @@ int rth_attn_decode_split(uint16_t* out, const uint16_t* q, const uint8_t* k,
                      "rth_attn_decode_split");
 }
 
+int rth_attn_decode_split_noalloc(uint16_t* out, const uint16_t* q, const uint8_t* k,
+                                  const uint8_t* v, const float* k_scale,
+                                  const float* v_scale, int num_splits,
+                                  const int* cache_len, int num_q_heads, int num_kv_heads,
+                                  int head_dim, float scale, void* stream) {
+    if (int rc = check_attn(out, q, k, v, k_scale, v_scale, cache_len)) {
+        return rc;
+    }
+    RTH_REQUIRE(num_splits >= 1 && num_splits <= 65536, "num_splits must be in [1, 65536]");
+    if (int rc = check_heads(num_q_heads, num_kv_heads)) {
+        return rc;
+    }
+    RTH_REQUIRE(head_dim == 32 || head_dim == 64 || head_dim == 128 || head_dim == 256 ||
+                    head_dim == 512,
+                "head_dim must be one of 32, 64, 128, 256, 512");
+    if (!rth::decode_mfma_supported(num_q_heads, num_kv_heads, head_dim)) {
+        // The naive kernel uses no scratch.
+        return check_hip(rth::attention_naive_launch(out, q, k, v, k_scale, v_scale, 1,
+                                                     cache_len, num_q_heads, num_kv_heads,
+                                                     head_dim, scale, as_stream(stream)),
+                         "rth_attn_decode_split_noalloc");
+    }
+    const std::size_t need = rth::decode_scratch_floats(num_q_heads, head_dim, num_splits);
+    RTH_REQUIRE(need <= rth::kNoAllocScratchFloats,
+                "rth_attn_decode_split_noalloc: num_q_heads * num_splits * (head_dim + 2) = " +
+                    std::to_string(need) + " floats exceeds the fixed scratch of " +
+                    std::to_string(rth::kNoAllocScratchFloats) + " floats");
+    float* partial = nullptr;
+    if (int rc = check_hip(rth::noalloc_scratch(&partial), "rth_attn_decode_split_noalloc")) {
+        return rc;
+    }
+    return check_hip(rth::flash_decode_launch(out, q, k, v, k_scale, v_scale, partial,
+                                              num_splits, cache_len, num_q_heads, num_kv_heads,
+                                              head_dim, scale, as_stream(stream)),
+                     "rth_attn_decode_split_noalloc");
+}
+
 int rth_attn_decode_append_split(uint16_t* out, const uint16_t* q, uint8_t* k_cache,
                                  uint8_t* v_cache, float* k_scale, float* v_scale,
                                  const uint16_t* k_new, const uint16_t* v_new,

@@ -42,6 +42,8 @@
 // merge folds the first n_eff = min(splits, tiles) slots. n_keys =
 // *cache_len + 1 is read on device, so one launch configuration serves every
 // decode step (graph capturable).
+#include <mutex>
+
 #include "device_common.hpp"
 #include "launch.hpp"
 
@@ -843,7 +845,40 @@ hipError_t launch_decode(uint16_t* out, const uint16_t* q, const uint8_t* k,
     return hipGetLastError();
 }
 
+// Decode scratch of the allocation-free entry point: one fixed array per
+// device, shared by every call on that device (the reference layout, the
+// first Hq*S*(D+2) floats in use). The kernels need it uninitialized, and
+// calls that overlap on one device race on it. In host code `scratch` is a
+// host-side stand-in: its device address comes from hipGetSymbolAddress.
+static __device__ __align__(256) float scratch[kNoAllocScratchFloats];
+
+constexpr int      kMaxScratchDevices = 64;
+std::mutex         g_scratch_mu;
+float*             g_scratch_ptr[kMaxScratchDevices];   // nullptr: not looked up yet
+
 }  // namespace
+
+hipError_t noalloc_scratch(float** ptr) {
+    int        dev = 0;
+    hipError_t e   = hipGetDevice(&dev);
+    if (e != hipSuccess) {
+        return e;
+    }
+    if (dev < 0 || dev >= kMaxScratchDevices) {
+        return hipErrorInvalidDevice;
+    }
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (g_scratch_ptr[dev] == nullptr) {
+        void* p = nullptr;
+        e       = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) {
+            return e;
+        }
+        g_scratch_ptr[dev] = static_cast<float*>(p);
+    }
+    *ptr = g_scratch_ptr[dev];
+    return hipSuccess;
+}
 
 std::size_t decode_scratch_floats(int num_q_heads, int head_dim, int max_splits) {
     const std::size_t hs = static_cast<std::size_t>(num_q_heads) *

@@ -34,6 +34,14 @@ hipError_t kv_append_fp8_launch(uint8_t* k_q, uint8_t* v_q, float* k_scale,
 // Split-K decode scratch in floats: [Hq, S] m, [Hq, S] l, [Hq, S, D] acc.
 std::size_t decode_scratch_floats(int num_q_heads, int head_dim, int max_splits);
 
+// Floats of the fixed per-device decode scratch (16 MiB) used by the
+// allocation-free decode entry point.
+constexpr std::size_t kNoAllocScratchFloats = std::size_t{1} << 22;
+
+// Device address of the current device's fixed decode scratch, looked up
+// with hipGetSymbolAddress on the first call per device.
+hipError_t noalloc_scratch(float** ptr);
+
 // k_new != nullptr: also append one token (k_new, v_new [Hkv, D] bf16) at row
 // *cache_len of the cache (k_w, v_w, ks_w, vs_w: the same slabs as k, v,
 // k_scale, v_scale) before attending over *cache_len + 1 keys.

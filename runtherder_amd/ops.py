@@ -87,6 +87,20 @@ def flash_decode_split_bf16(out, q, k, v, k_scale, v_scale, partial, num_splits,
               num_kv_heads, head_dim, float(scale), _stream(stream))
 
 
+def flash_decode_split_bf16_noalloc(out, q, k, v, k_scale, v_scale, num_splits, cache_len,
+                                    num_q_heads, num_kv_heads, head_dim, scale, stream=None):
+    """flash_decode_split_bf16 without caller scratch (no reference
+    counterpart): the partials live in the library's fixed per-device array,
+    shared by every call on the device (overlapping calls race)."""
+    _need(out, torch.bfloat16, "out"); _need(q, torch.bfloat16, "q")
+    _need(k, torch.uint8, "k"); _need(v, torch.uint8, "v")
+    _need(k_scale, torch.float32, "k_scale"); _need(v_scale, torch.float32, "v_scale")
+    _need(cache_len, torch.int32, "cache_len")
+    _ffi.call("rth_attn_decode_split_noalloc", _p(out), _p(q), _p(k), _p(v), _p(k_scale),
+              _p(v_scale), num_splits, _p(cache_len), num_q_heads, num_kv_heads, head_dim,
+              float(scale), _stream(stream))
+
+
 def flash_decode_append_split_bf16(out, q, k_cache, v_cache, k_scale, v_scale, k_new, v_new,
                                    partial, num_splits, cache_len, num_q_heads, num_kv_heads,
                                    head_dim, scale, stream=None):
