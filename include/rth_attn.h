@@ -82,13 +82,23 @@ int rth_default_num_splits(int num_kv_heads, int device);
  * log-sum-exp merge (two kernels: splits, then merge). `partial` is
  * caller-owned scratch of rth_split_scratch_floats(Hq, D, num_splits) floats.
  * head_dim in {32,64,128,256,512}; 64/128/256 with Hq/Hkv <= 16 run the MFMA
- * kernel, the rest the naive one. */
+ * split kernel, the rest the VALU split kernel (rth_decode_path). */
 int rth_attn_decode_split(uint16_t* out, const uint16_t* q, const uint8_t* k,
                           const uint8_t* v, const float* k_scale,
                           const float* v_scale, float* partial, int num_splits,
                           const int* cache_len, int num_q_heads,
                           int num_kv_heads, int head_dim, float scale,
                           void* stream);
+
+enum {
+    RTH_DECODE_MFMA = 1, /* bf16 MFMA split kernel */
+    RTH_DECODE_VALU = 2, /* VALU split kernel (DPP / shuffle reductions) */
+};
+
+/* No counterpart in the reference: which split kernel the decode entries run
+ * for this shape (RTH_DECODE_MFMA or RTH_DECODE_VALU), 0 if the shape is not
+ * supported. Lets a caller or a test tell the two paths apart. */
+int rth_decode_path(int num_q_heads, int num_kv_heads, int head_dim);
 
 /* No counterpart in the reference: rth_attn_decode_split without the
  * `partial` argument, for callers that cannot allocate (code under HIP graph

@@ -18,6 +18,9 @@ from .ops import (  # noqa: F401
     PagedKVCache,
     advance_position,
     attention_causal_bf16,
+    DECODE_MFMA,
+    DECODE_VALU,
+    decode_path,
     default_num_splits,
     flash_decode_append_split_bf16,
     flash_decode_split_bf16,

@@ -221,10 +221,24 @@ int rth_attn_decode_split(uint16_t* out, const uint16_t* q, const uint8_t* k,
                                                   as_stream(stream)),
                          "rth_attn_decode_split");
     }
-    return check_hip(rth::attention_naive_launch(out, q, k, v, k_scale, v_scale, 1,
-                                                 cache_len, num_q_heads, num_kv_heads,
-                                                 head_dim, scale, as_stream(stream)),
+    RTH_REQUIRE(partial != nullptr, "partial must not be null");
+    return check_hip(rth::flash_decode_valu_launch(out, q, k, v, k_scale, v_scale, partial,
+                                                   num_splits, cache_len, num_q_heads,
+                                                   num_kv_heads, head_dim, scale,
+                                                   as_stream(stream)),
                      "rth_attn_decode_split");
+}
+
+int rth_decode_path(int num_q_heads, int num_kv_heads, int head_dim) {
+    if (num_q_heads < 1 || num_kv_heads < 1 || num_q_heads % num_kv_heads != 0) {
+        return 0;
+    }
+    if (head_dim != 32 && head_dim != 64 && head_dim != 128 && head_dim != 256 &&
+        head_dim != 512) {
+        return 0;
+    }
+    return rth::decode_mfma_supported(num_q_heads, num_kv_heads, head_dim) ? RTH_DECODE_MFMA
+                                                                           : RTH_DECODE_VALU;
 }
 
 int rth_attn_decode_split_noalloc(uint16_t* out, const uint16_t* q, const uint8_t* k,
@@ -242,13 +256,6 @@ int rth_attn_decode_split_noalloc(uint16_t* out, const uint16_t* q, const uint8_
     RTH_REQUIRE(head_dim == 32 || head_dim == 64 || head_dim == 128 || head_dim == 256 ||
                     head_dim == 512,
                 "head_dim must be one of 32, 64, 128, 256, 512");
-    if (!rth::decode_mfma_supported(num_q_heads, num_kv_heads, head_dim)) {
-        // The naive kernel uses no scratch.
-        return check_hip(rth::attention_naive_launch(out, q, k, v, k_scale, v_scale, 1,
-                                                     cache_len, num_q_heads, num_kv_heads,
-                                                     head_dim, scale, as_stream(stream)),
-                         "rth_attn_decode_split_noalloc");
-    }
     const std::size_t need = rth::decode_scratch_floats(num_q_heads, head_dim, num_splits);
     RTH_REQUIRE(need <= rth::kNoAllocScratchFloats,
                 "rth_attn_decode_split_noalloc: num_q_heads * num_splits * (head_dim + 2) = " +
@@ -257,6 +264,13 @@ int rth_attn_decode_split_noalloc(uint16_t* out, const uint16_t* q, const uint8_
     float* partial = nullptr;
     if (int rc = check_hip(rth::noalloc_scratch(&partial), "rth_attn_decode_split_noalloc")) {
         return rc;
+    }
+    if (!rth::decode_mfma_supported(num_q_heads, num_kv_heads, head_dim)) {
+        return check_hip(rth::flash_decode_valu_launch(out, q, k, v, k_scale, v_scale, partial,
+                                                       num_splits, cache_len, num_q_heads,
+                                                       num_kv_heads, head_dim, scale,
+                                                       as_stream(stream)),
+                         "rth_attn_decode_split_noalloc");
     }
     return check_hip(rth::flash_decode_launch(out, q, k, v, k_scale, v_scale, partial,
                                               num_splits, cache_len, num_q_heads, num_kv_heads,
@@ -290,16 +304,18 @@ int rth_attn_decode_append_split(uint16_t* out, const uint16_t* q, uint8_t* k_ca
                                                   v_cache, k_scale, v_scale),
                          "rth_attn_decode_append_split");
     }
-    // Shapes without the MFMA decode: the append, then the naive kernel.
+    // Shapes without the MFMA decode: the append, then the VALU decode.
+    RTH_REQUIRE(partial != nullptr, "partial must not be null");
     if (int rc = check_hip(rth::kv_append_fp8_launch(k_cache, v_cache, k_scale, v_scale, k_new,
                                                      v_new, cache_len, num_kv_heads,
                                                      num_kv_heads, head_dim, as_stream(stream)),
                            "rth_attn_decode_append_split")) {
         return rc;
     }
-    return check_hip(rth::attention_naive_launch(out, q, k_cache, v_cache, k_scale, v_scale, 1,
-                                                 cache_len, num_q_heads, num_kv_heads,
-                                                 head_dim, scale, as_stream(stream)),
+    return check_hip(rth::flash_decode_valu_launch(out, q, k_cache, v_cache, k_scale, v_scale,
+                                                   partial, num_splits, cache_len, num_q_heads,
+                                                   num_kv_heads, head_dim, scale,
+                                                   as_stream(stream)),
                      "rth_attn_decode_append_split");
 }
 

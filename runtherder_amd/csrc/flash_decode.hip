@@ -190,6 +190,10 @@ __device__ __forceinline__ DecPartition dec_partition(int n_keys, int num_splits
         pt.coop   = true;
         pt.splits = num_splits;
         pt.gkv    = kvg;
+    } else if (kvg < 0) {   // the VALU kernel: one wave per unit at every context
+        pt.coop   = false;
+        pt.splits = num_splits;
+        pt.gkv    = 1;
     } else {
         const int coop_splits = n_wgs / hkv;
         pt.coop               = (n_keys <= kCoopMaxKeys) && (coop_splits >= 1);
@@ -801,6 +805,294 @@ __global__ __launch_bounds__(kCombineThreads) void flash_decode_combine_kernel(
     }
 }
 
+
+// ---- VALU split kernel -------------------------------------------------------
+// Serves the shapes the MFMA kernel does not (head_dim 32 and 512, GQA groups
+// above 16) with the same partition (one wave per (kv head, split, block of
+// kVGroup q heads) unit at every context; kvg = -1 for the merge), the same
+// scratch and the same merge kernel. No MFMA: a key row of D E4M3 bytes is
+// spread over D / 16 lanes, 16 bytes per lane (one coalesced 128-bit load of
+// K and one of V), so a wave takes 64 / (D / 16) keys per step. Each lane
+// converts its 16 codes exactly to bf16 (K) and fp32 (V) in registers, takes
+// its share of q . k with v_dot2c_f32_bf16, and the partial dots of a key
+// are summed by DPP row exchanges (quad_perm, row_half_mirror, row_mirror:
+// after each level every lane of the group holds the group sum) plus one
+// lane shuffle per level above 16 lanes. Every lane group
+// keeps its own online softmax over its keys (base 2, lazy reference as in
+// the MFMA kernel) and its 16 output columns of each q head; the lane groups
+// merge by lane shuffles at the end, and lane group 0 writes the partial.
+constexpr int kVGroup = 4;   // q heads per VALU unit
+
+template <int D>
+struct ValuTraits {
+    static_assert(D == 32 || D == 64 || D == 128 || D == 256 || D == 512,
+                  "VALU decode: D in {32, 64, 128, 256, 512}");
+    static constexpr int kLPK  = D / 16;         // lanes per key row
+    static constexpr int kKPS  = kWave / kLPK;   // keys per wave step
+    static constexpr int kRing = 4;              // steps in flight per wave
+};
+
+// Sum over aligned groups of N lanes (N a power of two <= 64); every lane of
+// a group ends with the group's sum.
+template <int N>
+__device__ __forceinline__ float group_sum(float v) {
+    if constexpr (N >= 2) {   // lanes xor 1
+        v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xF, 0xF, false));
+    }
+    if constexpr (N >= 4) {   // lanes xor 2
+        v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xF, 0xF, false));
+    }
+    if constexpr (N >= 8) {   // the other quad of the 8 (row_half_mirror)
+        v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x141, 0xF, 0xF, false));
+    }
+    if constexpr (N >= 16) {  // the other 8 of the row (row_mirror)
+        v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x140, 0xF, 0xF, false));
+    }
+    if constexpr (N >= 32) {
+        v += __shfl_xor(v, 16, kWave);
+    }
+    if constexpr (N >= 64) {
+        v += __shfl_xor(v, 32, kWave);
+    }
+    return v;
+}
+
+template <int D>
+struct ValuStep {
+    u32x4 kraw;
+    u32x4 vraw;
+    float ksc;
+    float vsc;
+};
+
+template <int D, bool kNT>
+__device__ __forceinline__ void valu_load(ValuStep<D>& st, const uint8_t* __restrict__ k,
+                                          const uint8_t* __restrict__ v,
+                                          const float* __restrict__ ks,
+                                          const float* __restrict__ vs, int key, int kvh,
+                                          int hkv, int j) {
+    const int64_t row = static_cast<int64_t>(key) * hkv + kvh;
+    st.kraw           = ld<kNT>(reinterpret_cast<const u32x4*>(k + row * D + 16 * j));
+    st.vraw           = ld<kNT>(reinterpret_cast<const u32x4*>(v + row * D + 16 * j));
+    st.ksc            = ks[row];
+    st.vsc            = vs[row];
+}
+
+template <int D>
+__global__ __launch_bounds__(kDecThreads) void flash_decode_valu_kernel(
+    const uint16_t* __restrict__ q, const uint8_t* __restrict__ k,
+    const uint8_t* __restrict__ v, const float* __restrict__ ks,
+    const float* __restrict__ vs, float* __restrict__ partial, int num_splits,
+    const int* __restrict__ cache_len, int hq, int hkv, float scale_log2) {
+    using T = ValuTraits<D>;
+    const int G    = hq / hkv;
+    const int nb   = (G + kVGroup - 1) / kVGroup;
+    const int tid  = static_cast<int>(threadIdx.x);
+    const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
+    const int lane = tid & (kWave - 1);
+    const int kl   = lane / T::kLPK;   // key of the step this lane works on
+    const int j    = lane % T::kLPK;   // 16-byte chunk of the row
+    // unit = ((split * hkv) + kv head) * nb + head block: the head blocks of
+    // one (kv head, split) are adjacent waves reading the same rows.
+    const int unit = static_cast<int>(blockIdx.x) * kDecWaves + wave;
+    const int hb   = unit % nb;
+    const int kvh  = (unit / nb) % hkv;
+    const int si   = unit / nb / hkv;
+
+    const int          n_keys = *cache_len + 1;
+    const DecPartition pt     = dec_partition(n_keys, num_splits, hkv, 0, -1);
+    if (si >= pt.n_eff) {
+        return;
+    }
+    const int k0 = split_tile(pt, si) * kTileKeys;
+    const int k1 = min(split_tile(pt, si + 1) * kTileKeys, n_keys);
+    const int h0 = hb * kVGroup;
+    const int gh = min(kVGroup, G - h0);
+
+    // q of the block's heads, this lane's 16 columns, as bf16 pairs.
+    bf16x2 qv[kVGroup][8];
+#pragma unroll
+    for (int h = 0; h < kVGroup; ++h) {
+        const uint16_t* qr = q + static_cast<int64_t>(kvh * G + h0 + min(h, gh - 1)) * D + 16 * j;
+        u32x4           w0 = *reinterpret_cast<const u32x4*>(qr);
+        u32x4           w1 = *reinterpret_cast<const u32x4*>(qr + 8);
+        if (h >= gh) {
+            w0 = u32x4{0u, 0u, 0u, 0u};
+            w1 = w0;
+        }
+        // Elements go through a scalar first: hipcc (ROCm 7.2) miscompiles
+        // __builtin_bit_cast of a vector subscript (it reads element 0).
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const uint32_t a = w0[e];
+            const uint32_t b = w1[e];
+            qv[h][e]         = __builtin_bit_cast(bf16x2, a);
+            qv[h][4 + e]     = __builtin_bit_cast(bf16x2, b);
+        }
+    }
+    float acc[kVGroup][16];
+    float m_run[kVGroup], l_run[kVGroup];
+#pragma unroll
+    for (int h = 0; h < kVGroup; ++h) {
+        m_run[h] = -INFINITY;
+        l_run[h] = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+            acc[h][e] = 0.0f;
+        }
+    }
+
+    constexpr float kLazy  = 8.0f;
+    auto            process = [&](const ValuStep<D>& st, int key) {
+        const bool valid = key < k1;
+        // K codes -> 8 bf16 pairs (exact).
+        bf16x2 kb[8];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            kb[2 * e]     = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(st.kraw[e], 1.0f, false);
+            kb[2 * e + 1] = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(st.kraw[e], 1.0f, true);
+        }
+        // V codes -> 16 fp32 (exact).
+        float vf[16];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const f32x2 lo = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(st.vraw[e], 1.0f, false);
+            const f32x2 hi = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(st.vraw[e], 1.0f, true);
+            vf[4 * e]      = lo.x;
+            vf[4 * e + 1]  = lo.y;
+            vf[4 * e + 2]  = hi.x;
+            vf[4 * e + 3]  = hi.y;
+        }
+        const float kf = st.ksc * scale_log2;
+#pragma unroll
+        for (int h = 0; h < kVGroup; ++h) {
+            float sd = 0.0f;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                sd = __builtin_amdgcn_fdot2_f32_bf16(qv[h][e], kb[e], sd, false);
+            }
+            const float x = group_sum<T::kLPK>(sd) * kf;
+            if (valid && x > m_run[h] + kLazy) {
+                const float alpha = __builtin_amdgcn_exp2f(m_run[h] - x);
+                l_run[h] *= alpha;
+#pragma unroll
+                for (int e = 0; e < 16; ++e) {
+                    acc[h][e] *= alpha;
+                }
+                m_run[h] = x;
+            }
+            const float p = valid ? __builtin_amdgcn_exp2f(x - m_run[h]) : 0.0f;
+            l_run[h] += p;
+            const float pv = p * st.vsc;
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                acc[h][e] = fmaf(pv, vf[e], acc[h][e]);
+            }
+        }
+    };
+
+    const int n_steps = (k1 - k0 + T::kKPS - 1) / T::kKPS;
+    if (n_steps > 0) {
+        auto key_of_step = [&](int st) { return k0 + st * T::kKPS + kl; };
+        auto stream      = [&]<bool kNT>() {
+            constexpr int  R = T::kRing;
+            ValuStep<D>    ring[R];
+            const int      last = n_steps - 1;
+#pragma unroll
+            for (int r = 0; r + 1 < R; ++r) {
+                const int key = min(key_of_step(min(r, last)), k1 - 1);
+                valu_load<D, kNT>(ring[r], k, v, ks, vs, key, kvh, hkv, j);
+            }
+            for (int t = 0;; t += R) {
+                bool done = false;
+#pragma unroll
+                for (int r = 0; r < R; ++r) {
+                    if (!done) {
+                        const int tr  = t + r;
+                        const int key = min(key_of_step(min(tr + R - 1, last)), k1 - 1);
+                        valu_load<D, kNT>(ring[(r + R - 1) % R], k, v, ks, vs, key, kvh, hkv,
+                                          j);
+                        process(ring[r], key_of_step(tr));
+                        done = tr >= last;
+                    }
+                }
+                if (done) {
+                    break;
+                }
+            }
+        };
+        if (n_steps > 4 * kNtMinTiles) {
+            stream.template operator()<true>();
+        } else {
+            stream.template operator()<false>();
+        }
+    }
+
+    // Merge the lane groups (lanes j, j + kLPK, ... hold the same columns).
+#pragma unroll
+    for (int mask = T::kLPK; mask < kWave; mask <<= 1) {
+#pragma unroll
+        for (int h = 0; h < kVGroup; ++h) {
+            const float m2 = __shfl_xor(m_run[h], mask, kWave);
+            const float l2 = __shfl_xor(l_run[h], mask, kWave);
+            const float M  = fmaxf(m_run[h], m2);
+            const float f1 = (m_run[h] == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(m_run[h] - M);
+            const float f2 = (m2 == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(m2 - M);
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                const float a2 = __shfl_xor(acc[h][e], mask, kWave);
+                acc[h][e]      = acc[h][e] * f1 + a2 * f2;
+            }
+            l_run[h] = l_run[h] * f1 + l2 * f2;
+            m_run[h] = M;
+        }
+    }
+    if (kl == 0) {
+        const int64_t hs     = static_cast<int64_t>(hq) * num_splits;
+        float*        part_m = partial;
+        float*        part_l = partial + hs;
+        float*        part_o = partial + 2 * hs;
+#pragma unroll
+        for (int h = 0; h < kVGroup; ++h) {
+            if (h < gh) {
+                const int64_t slot = static_cast<int64_t>(kvh * G + h0 + h) * num_splits + si;
+                float*        o    = part_o + slot * D + 16 * j;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    *reinterpret_cast<f32x4*>(o + 4 * e) =
+                        f32x4{acc[h][4 * e], acc[h][4 * e + 1], acc[h][4 * e + 2], acc[h][4 * e + 3]};
+                }
+                if (j == 0) {
+                    part_m[slot] = m_run[h];
+                    part_l[slot] = l_run[h];
+                }
+            }
+        }
+    }
+}
+
+template <int D>
+hipError_t launch_decode_valu(uint16_t* out, const uint16_t* q, const uint8_t* k,
+                              const uint8_t* v, const float* ks, const float* vs,
+                              float* partial, int num_splits, const int* cache_len, int hq,
+                              int hkv, float scale, hipStream_t stream) {
+    const int     nb    = (hq / hkv + kVGroup - 1) / kVGroup;
+    const int64_t units = static_cast<int64_t>(num_splits) * hkv * nb;
+    const int     n_wgs = static_cast<int>((units + kDecWaves - 1) / kDecWaves);
+    hipLaunchKernelGGL(flash_decode_valu_kernel<D>, dim3(static_cast<unsigned>(n_wgs)),
+                       dim3(kDecThreads), 0, stream, q, k, v, ks, vs, partial, num_splits,
+                       cache_len, hq, hkv, scale * kLog2e);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) {
+        return e;
+    }
+    hipLaunchKernelGGL(flash_decode_combine_kernel<D>,
+                       dim3(static_cast<unsigned>(hq), static_cast<unsigned>(D / kCombineSlice)),
+                       dim3(kCombineThreads), 0, stream, out, partial, num_splits, cache_len,
+                       hq, hkv, 0, -1);
+    return hipGetLastError();
+}
+
 __global__ void advance_position_kernel(int* pos, int delta) {
     if (threadIdx.x == 0 && blockIdx.x == 0) {
         *pos += delta;
@@ -918,6 +1210,27 @@ hipError_t flash_decode_launch(uint16_t* out, const uint16_t* q,
         RTH_DEC_CASE(128)
         RTH_DEC_CASE(256)
 #undef RTH_DEC_CASE
+        default:
+            return hipErrorInvalidValue;
+    }
+}
+
+hipError_t flash_decode_valu_launch(uint16_t* out, const uint16_t* q, const uint8_t* k,
+                                   const uint8_t* v, const float* k_scale,
+                                   const float* v_scale, float* partial, int num_splits,
+                                   const int* cache_len, int num_q_heads, int num_kv_heads,
+                                   int head_dim, float scale, hipStream_t stream) {
+    switch (head_dim) {
+#define RTH_VALU_CASE(DD)                                                                     \
+    case DD:                                                                                  \
+        return launch_decode_valu<DD>(out, q, k, v, k_scale, v_scale, partial, num_splits,   \
+                                      cache_len, num_q_heads, num_kv_heads, scale, stream);
+        RTH_VALU_CASE(32)
+        RTH_VALU_CASE(64)
+        RTH_VALU_CASE(128)
+        RTH_VALU_CASE(256)
+        RTH_VALU_CASE(512)
+#undef RTH_VALU_CASE
         default:
             return hipErrorInvalidValue;
     }

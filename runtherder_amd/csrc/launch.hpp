@@ -57,6 +57,15 @@ hipError_t flash_decode_launch(uint16_t* out, const uint16_t* q,
                                float* vs_w = nullptr, const int* block_table = nullptr,
                                int block_shift = 0);
 
+// The VALU split kernel + merge: head_dim in {32, 64, 128, 256, 512}, any
+// GQA group (no paging, no fused append). The decode entry points use it for
+// the shapes decode_mfma_supported rejects.
+hipError_t flash_decode_valu_launch(uint16_t* out, const uint16_t* q, const uint8_t* k,
+                                   const uint8_t* v, const float* k_scale,
+                                   const float* v_scale, float* partial, int num_splits,
+                                   const int* cache_len, int num_q_heads, int num_kv_heads,
+                                   int head_dim, float scale, hipStream_t stream);
+
 // block_table != nullptr: paged cache, logical block b (2^block_shift keys)
 // stored at physical block block_table[b] (same for the decode launch).
 hipError_t flash_prefill_launch(uint16_t* out, const uint16_t* q,

@@ -87,6 +87,15 @@ def flash_decode_split_bf16(out, q, k, v, k_scale, v_scale, partial, num_splits,
               num_kv_heads, head_dim, float(scale), _stream(stream))
 
 
+DECODE_MFMA, DECODE_VALU = 1, 2
+
+
+def decode_path(num_q_heads: int, num_kv_heads: int, head_dim: int) -> int:
+    """Which split kernel decode runs for the shape: DECODE_MFMA, DECODE_VALU
+    or 0 (unsupported). No reference counterpart."""
+    return int(_ffi.load().rth_decode_path(num_q_heads, num_kv_heads, head_dim))
+
+
 def flash_decode_split_bf16_noalloc(out, q, k, v, k_scale, v_scale, num_splits, cache_len,
                                     num_q_heads, num_kv_heads, head_dim, scale, stream=None):
     """flash_decode_split_bf16 without caller scratch (no reference

@@ -171,6 +171,38 @@ def test_grouped_workgroups(ctx, hq, hkv, splits):
     check(got, q, k8, v8, ks, vs, ctx - 1, hq, hkv, d, scale)
 
 
+@pytest.mark.parametrize("cache_len,hq,hkv,d,splits", [
+    (8191, 8, 2, 32, None), (131071, 32, 8, 32, 64), (9000, 16, 4, 512, 64),
+    (65535, 8, 2, 512, None), (10000, 64, 2, 128, None), (5000, 40, 2, 64, 100),
+    (40, 32, 8, 32, 4), (3, 8, 2, 512, 8), (2999, 68, 4, 256, 32),
+])
+def test_valu_split_kernel(cache_len, hq, hkv, d, splits):
+    """Shapes the MFMA split kernel does not take (head_dim 32 and 512, GQA
+    groups above 16) run the VALU split kernel (reference
+    src/kernels/flash_decode.cu:296-319 serves all five head sizes with one
+    split kernel): contexts up to 128K, ragged head blocks (20 and 17 q heads
+    per kv head), more splits than tiles."""
+    assert R.decode_path(hq, hkv, d) == R.DECODE_VALU
+    scale = np.float32(1.0 / np.sqrt(d))
+    splits = splits or R.default_num_splits(hkv)
+    q = O.normal_bf16((hq, d), 91 + d)
+    _, _, k8, v8, ks, vs = make_cache(cache_len + 1, hkv, d, kind="normal", seed=cache_len)
+    got = gpu_decode(q, k8, v8, ks, vs, cache_len, hq, hkv, d, splits, scale)
+    check(got, q, k8, v8, ks, vs, cache_len, hq, hkv, d, scale)
+
+
+def test_decode_path_selection():
+    """The reference test shapes with head_dim 32 / 512 take the VALU kernel;
+    head_dim 64 / 128 / 256 with groups up to 16 the MFMA kernel."""
+    assert R.decode_path(32, 8, 32) == R.DECODE_VALU
+    assert R.decode_path(8, 2, 512) == R.DECODE_VALU
+    assert R.decode_path(64, 2, 128) == R.DECODE_VALU
+    for d in (64, 128, 256):
+        assert R.decode_path(32, 8, d) == R.DECODE_MFMA
+    assert R.decode_path(64, 4, 128) == R.DECODE_MFMA
+    assert R.decode_path(30, 8, 128) == 0 and R.decode_path(32, 8, 96) == 0
+
+
 def test_repeated_calls_share_scratch():
     """Back-to-back calls with different depths on one scratch stay correct
     (the scratch carries no state between calls)."""

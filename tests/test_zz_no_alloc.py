@@ -57,6 +57,7 @@ def test_noalloc_equals_caller_scratch_on_consecutive_calls():
     run_both(40000, 32, 8, 128, 256, 900)
     run_both(3000, 24, 8, 128, 64, 910)
     run_both(9000, 16, 8, 256, 100, 920)
+    run_both(5000, 16, 4, 32, 64, 930)     # the VALU split kernel
 
 
 def test_noalloc_rejects_oversized_scratch():
