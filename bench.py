@@ -13,6 +13,12 @@ Algorithmic units (no credit for re-reads or scratch):
   decode bytes / call  = ctx*Hkv*D*2 + ctx*Hkv*8 + Hq*D*4
   prefill flops / call = 4*Hq*D*P, P = n*clen + n*(n+1)/2
 
+Timed steps are exactly --steps (full 128-step graphs plus one graph of the
+remainder), after exactly --warmup untimed steps. The line also carries the
+roofline of the decode call at 32768 and 131072 keys and of prefill at 8192
+and 16384 tokens ("target_range"), and CPU baselines for decode (GB/s) and
+prefill (GFLOP/s).
+
 Prints one JSON line. Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
 """
 from __future__ import annotations
@@ -108,8 +114,8 @@ def bench_decode(torch, R, args, stream):
         pos.fill_(depth)
     torch.cuda.synchronize()
 
-    def run_steps(fused):
-        for s in range(GRAPH_STEPS):
+    def run_steps(fused, n_steps):
+        for s in range(n_steps):
             for l in range(L):
                 if fused:
                     backend.run_decode_append(out[s, l], qs[s, l], cache.view(l), ks[s, l],
@@ -118,31 +124,40 @@ def bench_decode(torch, R, args, stream):
                     cache.append(l, ks[s, l], vs[s, l], 1, pos)
                     backend.run(out[s, l], qs[s, l], cache.view(l), 1, pos)
             R.advance_position(pos, 1)
-        R.advance_position(pos, -GRAPH_STEPS)   # replays are idempotent
+        R.advance_position(pos, -n_steps)   # replays are idempotent
 
-    replays_w = max(1, math.ceil(args.warmup / GRAPH_STEPS))
-    replays = max(1, math.ceil(args.steps / GRAPH_STEPS))
+    # Exactly args.steps timed steps (and args.warmup untimed ones): full
+    # 128-step graphs plus one graph of the remainder.
+    steps = max(1, args.steps)
     step_bytes = [sum(decode_bytes(ctx0 + s, hq, hkv, d) for _ in range(L))
                   for s in range(GRAPH_STEPS)]
-    total_bytes = replays * sum(step_bytes)
+    full, rem = divmod(steps, GRAPH_STEPS)
+    total_bytes = full * sum(step_bytes) + sum(step_bytes[:rem])
+    w_full, w_rem = divmod(max(0, args.warmup), GRAPH_STEPS)
     timed = {}
     for fused in (False, True):
-        graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(graph, stream=stream):
-            run_steps(fused)
+        graphs = {}
+        for n in {GRAPH_STEPS, rem, w_rem} - {0}:
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g, stream=stream):
+                run_steps(fused, n)
+            graphs[n] = g
         torch.cuda.synchronize()
         with torch.cuda.stream(stream):
-            for _ in range(replays_w):
-                graph.replay()
+            for _ in range(w_full):
+                graphs[GRAPH_STEPS].replay()
+            if w_rem:
+                graphs[w_rem].replay()
         torch.cuda.synchronize()
         with torch.cuda.stream(stream):
             with EventTimer(torch, stream) as t:
-                for _ in range(replays):
-                    graph.replay()
+                for _ in range(full):
+                    graphs[GRAPH_STEPS].replay()
+                if rem:
+                    graphs[rem].replay()
         torch.cuda.synchronize()
         timed[fused] = t.ms
-        del graph
-    steps = replays * GRAPH_STEPS
+        del graphs
     ms_per_step = timed[True] / steps
     value_gbs = total_bytes / (timed[True] * 1e-3) / 1e9
     unfused_gbs = total_bytes / (timed[False] * 1e-3) / 1e9
@@ -170,7 +185,7 @@ def bench_decode(torch, R, args, stream):
     return {
         "value": value_gbs, "ms_per_step": ms_per_step, "steps": steps,
         "unfused_value": unfused_gbs, "unfused_ms_per_step": timed[False] / steps,
-        "warmup": replays_w * GRAPH_STEPS, "ctx": ctx0, "splits": backend.num_splits,
+        "warmup": max(0, args.warmup), "ctx": ctx0, "splits": backend.num_splits,
         "kernel_us": kern_us, "kernel_bytes": kbytes, "kernel_gbs": achieved,
         "cache": cache, "qs": qs, "depth": depth, "hq": hq, "hkv": hkv, "d": d,
         "scale": scale, "out": out, "backend": backend, "pos": pos,
@@ -266,7 +281,7 @@ def bench_rope_append(torch, R, stream, n=4096, iters=20):
     return res
 
 
-def decode_kernel_sweep(torch, R, stream, points):
+def decode_kernel_sweep(torch, R, stream, points, quiet=False):
     """Per-call decode time (split kernel + merge kernel) at several context
     depths, rotating over enough layers that the working set exceeds the
     256 MB Infinity Cache. points: (hq, hkv, ctx, splits or None)."""
@@ -302,7 +317,8 @@ def decode_kernel_sweep(torch, R, stream, points):
         res.append({"hq": hq, "hkv": hkv, "ctx": ctx, "splits": backend.num_splits,
                     "layers": L, "us": round(us, 2), "gbs": round(nbytes / us / 1e3, 1),
                     "frac": round(nbytes / us / 1e3 / PEAK_HBM_GBS, 4)})
-        print(json.dumps({"decode_sweep": res[-1]}), flush=True)
+        if not quiet:
+            print(json.dumps({"decode_sweep": res[-1]}), flush=True)
         del cache, backend, q, out
         torch.cuda.empty_cache()
     return res
@@ -365,9 +381,9 @@ def eager_kernels(torch, R, stream, args):
     return 0
 
 
-def profile_traffic():
-    """HBM bytes per decode call from the committed PMC summary, if present."""
-    f = ROOT / "profiles" / "decode_attn_8k_pmc_traffic.md"
+def profile_traffic(name="decode_attn_8k_pmc_traffic.md"):
+    """HBM bytes per decode call from a committed PMC summary, if present."""
+    f = ROOT / "profiles" / name
     if not f.exists():
         return None
     for line in f.read_text().splitlines():
@@ -412,6 +428,66 @@ def cpu_baseline(torch, dec, budget_s=10.0):
                       f"{t_total:.1f} s on {cores} threads"}
 
 
+def cpu_prefill_baseline(budget_s=6.0):
+    """The oracle's naive fp32 causal attention (reference
+    src/kernels/attention.cu:34-91) on config 2's shape (n=1021, 24Q/8KV,
+    head_dim 128, FP8 cache from the oracle's quantizer) on host threads,
+    repeated for about budget_s seconds; GFLOP/s in the algorithmic units of
+    the GPU prefill figure."""
+    sys.path.insert(0, str(ROOT / "tests"))
+    import numpy as np
+    import oracle_lib as O
+
+    cores = max(1, min(16, os.cpu_count() or 1))
+    n, hq, hkv, d = 1021, 24, 8, 128
+    q = O.normal_bf16((n, hq, d), 71)
+    k8, ks = O.quantize_kv_fp8(O.normal_bf16((n * hkv, d), 72), d)
+    v8, vs = O.quantize_kv_fp8(O.normal_bf16((n * hkv, d), 73), d)
+    scale = np.float32(1.0 / math.sqrt(d))
+    calls, t_total = 0, 0.0
+    while t_total < budget_s and calls < 200:
+        t0 = time.perf_counter()
+        O.attention_f32(q, k8, v8, ks, vs, n, 0, hq, hkv, d, scale, cores)
+        t_total += time.perf_counter() - t0
+        calls += 1
+    fl = calls * prefill_flops(n, 0, hq, d)
+    return {"value": round(fl / t_total / 1e9, 2), "unit": "GFLOP/s", "cores": cores,
+            "kind": "port", "ms_per_call": round(1e3 * t_total / calls, 1),
+            "sample": f"{calls} calls of config 2 (n=1021, 24Q/8KV, causal, clen 0), fp32 "
+                      f"two-pass naive attention over the FP8 cache, {t_total:.1f} s on "
+                      f"{cores} threads"}
+
+
+def extra_rooflines(torch, R, stream):
+    """The north star's target ranges beyond the headline points, each with
+    its roofline: decode per call at ctx 32768 (config 3, 24Q/8KV, default
+    splits) and 131072 (config 5, 32Q/8KV, the config's 64 splits; per-head
+    scales do not change the work), prefill at 8192 and 16384 (config 4)."""
+    out = []
+    for hq, hkv, ctx, splits, cfg in ((24, 8, 32768, None, "config3"),
+                                      (32, 8, 131072, 64, "config5"),
+                                      (32, 8, 131072, None, "config5 default splits")):
+        pt = decode_kernel_sweep(torch, R, stream, [(hq, hkv, ctx, splits)], quiet=True)[0]
+        out.append({"kind": "decode", "workload": f"{cfg}: decode {hq}Q/{hkv}KV ctx {ctx}, "
+                                                  f"{pt['splits']} splits",
+                    "us": pt["us"],
+                    "roofline": {"bound": "hbm", "achieved": pt["gbs"], "peak": PEAK_HBM_GBS,
+                                 "unit": "GB/s", "frac": pt["frac"],
+                                 "bytes_per_launch": decode_bytes(ctx, hq, hkv, 128),
+                                 "traffic": (profile_traffic("decode_attn_128k_pmc_traffic.md")
+                                             if (ctx == 131072 and splits == 64) else None)}})
+    for n in (8192, 16384):
+        pf = bench_prefill(torch, R, stream, n=n)
+        out.append({"kind": "prefill", "workload": f"config4: prefill 32Q/8KV n={n}, clen 0",
+                    "us": round(pf["us"], 1),
+                    "roofline": {"bound": "mfma", "achieved": round(pf["tflops"], 1),
+                                 "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                                 "frac": round(pf["tflops"] / PEAK_BF16_TFLOPS, 4),
+                                 "flops_per_launch": pf["flops"]}})
+        torch.cuda.empty_cache()
+    return out
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -453,7 +529,9 @@ def main() -> int:
     dec = bench_decode(torch, R, args, stream)
     pf = bench_prefill(torch, R, stream, n=args.prefill_n)
     ra = bench_rope_append(torch, R, stream, n=args.prefill_n)
+    extra = extra_rooflines(torch, R, stream)
     cpu = None if args.no_cpu else cpu_baseline(torch, dec)
+    cpu_pf = None if args.no_cpu else cpu_prefill_baseline()
 
     line = {
         "metric": "decode attn HBM GB/s (% peak) @8K ctx; prefill attn TFLOP/s @4K tok",
@@ -466,7 +544,7 @@ def main() -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "e4m3-kv/bf16-mfma/fp32-acc",
+        "dtype": "e4m3-kv/decode-bf16-mfma/prefill-fp8(qk,exact-q-split)+f16(pv)-mfma/fp32-acc",
         "data": "synthetic: N(0,1) bf16 q/k/v, k/v quantized to FP8 E4M3 by the append kernel",
         "config": {
             "workload": "config3: 28-layer Llama-3.2-3B-shaped decode attention, 24Q/8KV, "
@@ -493,7 +571,9 @@ def main() -> int:
                          "frac": round(pf["tflops"] / PEAK_BF16_TFLOPS, 4),
                          "flops_per_launch": pf["flops"]},
             "append_us": round(pf["append_us"], 2), "append_gbs": round(pf["append_gbs"], 1),
+            "cpu_baseline": cpu_pf,
         },
+        "target_range": extra,
         "rope_append": dict(ra, workload="config4 shapes: RoPE(q,k) + K/V FP8 append (and the "
                                          "Qwen3 q/k RMSNorm before it), fused entries vs the "
                                          "unfused launch sequences"),

@@ -403,13 +403,21 @@ __global__ __launch_bounds__(kWaves * kWave, kSplit ? 1 : 2) void flash_prefill_
     // score more than 15 above m_ref); otherwise the tile needs no max
     // reduction, no cross-lane step and no rescale of l and O. Every p and l
     // use the same m_ref, and p <= 2^15 keeps every p inside the f16 range.
-    auto softmax = [&](f32x16 (&sx)[2], const float* kfb, int kt, f16x8 (&pop)[4]) {
+    // The k-factors of the 32 keys a lane holds, read before the score MFMAs
+    // so that the LDS latency hides behind them.
+    auto load_kf = [&](const float* kfb, f32x4 (&kfv)[8]) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            kfv[i] = *reinterpret_cast<const f32x4*>(kfb + 32 * (i >> 2) + 8 * (i & 3) + 4 * h);
+        }
+    };
+    auto softmax = [&](f32x16 (&sx)[2], const f32x4 (&kfv)[8], int kt, f16x8 (&pop)[4]) {
         const int key0 = kt * kBN;
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb) {
 #pragma unroll
             for (int rg = 0; rg < 4; ++rg) {
-                const f32x4 f = *reinterpret_cast<const f32x4*>(kfb + 32 * kb + 8 * rg + 4 * h);
+                const f32x4 f = kfv[4 * kb + rg];
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
                     sx[kb][4 * rg + e] = fmaf(sx[kb][4 * rg + e], f[e], -m_ref);
@@ -568,8 +576,10 @@ __global__ __launch_bounds__(kWaves * kWave, kSplit ? 1 : 2) void flash_prefill_
                 if (kt < w_tiles) {
                     f32x16 sx[2];
                     f16x8  pop[4];
+                    f32x4  kfv[8];
+                    load_kf(kfb, kfv);
                     qk(kcur, sx);
-                    softmax(sx, kfb, kt, pop);
+                    softmax(sx, kfv, kt, pop);
                     pv(vtb, pop);
                 }
                 // K(kt + 1), copied during the previous tile, must have landed;
@@ -603,8 +613,10 @@ __global__ __launch_bounds__(kWaves * kWave, kSplit ? 1 : 2) void flash_prefill_
                 v_tile_load<kGThreads>(rawc, v, ks, vs, r2, kvh, hkv, gtid);
                 if (kt < w_tiles) {
                     f32x16 sx[2];
+                    f32x4  kfv[8];
+                    load_kf(kfb, kfv);
                     qk(kcur, sx);
-                    softmax(sx, kfb, kt, pop_keep);
+                    softmax(sx, kfv, kt, pop_keep);
                 }
                 v_tile_stage<kGThreads>(rawn, vnext, nkf, gtid, scale_log2);
                 lds_barrier();
@@ -718,7 +730,9 @@ __global__ __launch_bounds__(kWaves * kWave, kSplit ? 1 : 2) void flash_prefill_
                 }
 
                 f16x8 pop[4];
-                softmax(s, kf, kt, pop);
+                f32x4 kfv[8];
+                load_kf(kf, kfv);
+                softmax(s, kfv, kt, pop);
 
                 // O^T += V^T P^T.
 #pragma unroll
