@@ -113,3 +113,60 @@ def test_decode_steps_in_one_hip_graph():
                                cfg.scale, NTHREADS)
         mx, mean = O.bf16_err(eager[-1, l], want[0])
         assert mx <= 2e-2 and mean <= 2e-3, (l, mx, mean)
+
+
+def test_config3_28_layer_128_step_graph():
+    """BASELINE config 3 at depth 8196: 28 layers x 128 decode steps (fused
+    one-token append + split-K decode per layer, device-side position advance)
+    captured in one HIP graph. After one replay, every appended cache row
+    equals the oracle quantizer's bytes and the last step of all 28 layers
+    matches the oracle's attention over the whole cache."""
+    layers, steps, depth = 28, 128, 8195
+    cfg = R.AttnConfig.for_heads(HQ, HKV, D)
+    backend = R.AdaptiveAttention(cfg)
+    cache = R.KVCache(layers, depth + steps, HKV, D)
+    pos = int_dev(0)
+    gen = torch.Generator(device=DEV)
+    gen.manual_seed(8196)
+    step("config3 graph: history fill")
+    for l in range(layers):
+        k = torch.randn((depth, HKV, D), generator=gen, device=DEV).to(torch.bfloat16)
+        v = torch.randn((depth, HKV, D), generator=gen, device=DEV).to(torch.bfloat16)
+        cache.append(l, k, v, depth, pos)
+    qs = torch.randn((steps, layers, HQ, D), generator=gen, device=DEV).to(torch.bfloat16)
+    kn = torch.randn((steps, layers, HKV, D), generator=gen, device=DEV).to(torch.bfloat16)
+    vn = torch.randn((steps, layers, HKV, D), generator=gen, device=DEV).to(torch.bfloat16)
+    outs = torch.zeros((steps, layers, HQ, D), dtype=torch.bfloat16, device=DEV)
+    sync()
+    stream = torch.cuda.Stream()
+    g = torch.cuda.CUDAGraph()
+    step("config3 graph: capture")
+    with torch.cuda.graph(g, stream=stream):
+        for s in range(steps):
+            for l in range(layers):
+                backend.run_decode_append(outs[s, l], qs[s, l], cache.view(l), kn[s, l],
+                                          vn[s, l], pos)
+            R.advance_position(pos, 1)
+    pos.fill_(depth)
+    sync()
+    step("config3 graph: replay")
+    g.replay()
+    sync()
+    assert int(pos.item()) == depth + steps
+    kn_h, vn_h = bf16_host(kn), bf16_host(vn)
+    q_last = bf16_host(qs[-1])
+    out_last = bf16_host(outs[-1])
+    for l in range(layers):
+        view = cache.view(l)
+        k8, v8 = host(view.k).reshape(-1, D), host(view.v).reshape(-1, D)
+        ks, vs = host(view.k_scale).reshape(-1), host(view.v_scale).reshape(-1)
+        rows = slice(depth * HKV, (depth + steps) * HKV)
+        wk, wks = O.quantize_kv_fp8(kn_h[:, l].reshape(-1, D), D)
+        wv, wvs = O.quantize_kv_fp8(vn_h[:, l].reshape(-1, D), D)
+        assert np.array_equal(k8[rows], wk) and np.array_equal(v8[rows], wv), l
+        assert np.array_equal(ks[rows].view(np.uint32), wks.view(np.uint32)), l
+        assert np.array_equal(vs[rows].view(np.uint32), wvs.view(np.uint32)), l
+        want = O.attention_f32(q_last[l], k8, v8, ks, vs, 1, depth + steps - 1, HQ, HKV, D,
+                               cfg.scale, NTHREADS)
+        mx, mean = O.bf16_err(out_last[l], want[0])
+        assert mx <= 2e-2 and mean <= 2e-3, (l, mx, mean)

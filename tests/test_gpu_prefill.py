@@ -226,6 +226,14 @@ def check_rows(got, q, k8, v8, ks, vs, clen, rows, hq, hkv, d, scale):
     return worst
 
 
+def check_block(got, q, k8, v8, ks, vs, clen, r0, r1, hq, hkv, d, scale):
+    """Rows r0..r1-1 (every head) against the oracle in one call."""
+    want = O.attention_f32(q[r0:r1], k8, v8, ks, vs, r1 - r0, clen + r0, hq, hkv, d, scale,
+                           NTHREADS)
+    mx, mean = O.bf16_err(got[r0:r1], want)
+    assert mx <= MAX_ABS and mean <= MEAN_ABS, (r0, r1, mx, mean)
+
+
 @pytest.mark.parametrize("n", [2048, 4096, 8192, 16384])
 def test_config4_prefill_sampled_rows(n):
     """32Q/8KV, RoPE theta 1e6, FP8 writeback; oracle on sampled rows."""
@@ -240,7 +248,11 @@ def test_config4_prefill_sampled_rows(n):
     sync()
     k8, v8 = host(view.k).reshape(-1, d), host(view.v).reshape(-1, d)
     ks, vs = host(view.k_scale).reshape(-1), host(view.v_scale).reshape(-1)
-    check_rows(bf16_host(out), q, k8, v8, ks, vs, 0, sampled_rows(n, 12, n), hq, hkv, d, scale)
+    got = bf16_host(out)
+    check_rows(got, q, k8, v8, ks, vs, 0, sampled_rows(n, 12, n), hq, hkv, d, scale)
+    if n == 16384:
+        # The heaviest workgroup's rows (the last 256, every head) in full.
+        check_block(got, q, k8, v8, ks, vs, 0, n - 256, n, hq, hkv, d, scale)
 
 
 @pytest.mark.parametrize("clen", [0, 37, 100, 165])
@@ -338,4 +350,31 @@ def test_config5_chunked_prefill_into_128k_cache():
     ks, vs = host(view.k_scale).reshape(-1), host(view.v_scale).reshape(-1)
     wk = O.quantize_kv_fp8_scaled(hist_k, pks, d)
     assert np.array_equal(k8[: clen * hkv], wk)
-    check_rows(bf16_host(out), q, k8, v8, ks, vs, clen, sampled_rows(n, 4, 5), hq, hkv, d, scale)
+    got = bf16_host(out)
+    check_rows(got, q, k8, v8, ks, vs, clen, sampled_rows(n, 4, 5), hq, hkv, d, scale)
+    # The heaviest workgroup's rows (the last 256 of the chunk, every head).
+    check_block(got, q, k8, v8, ks, vs, clen, n - 256, n, hq, hkv, d, scale)
+
+
+@pytest.mark.parametrize("mag", [2.0 ** -10, 1.0, 2.0 ** 13])
+def test_value_magnitudes_within_f16_staging(mag):
+    """V is staged for the P V MFMAs as f16(code * v_scale), as the reference
+    stages it (flash_prefill.cuh:21-24): values with |v| inside the f16 normal
+    range [2^-14, 65504] keep full precision. Rows of N(0,1) * mag (|v| up to
+    ~4.5 * 2^13 = 37k at the top) match the oracle within the tolerance
+    relative to mag. Outside that range (|v| > 65504, or far below 2^-14)
+    prefill is not supported, like the reference; decode has no such limit
+    (bf16 V with the scale folded into P)."""
+    n, hq, hkv, d = 600, 8, 2, 128
+    scale = np.float32(1.0 / np.sqrt(d))
+    q = O.normal_bf16((n, hq, d), 81)
+    k8, ks = O.quantize_kv_fp8(O.normal_bf16((n * hkv, d), 82), d)
+    vx = O.f32_to_bf16(O.bf16_to_f32(O.normal_bf16((n * hkv, d), 83)) * np.float32(mag))
+    v8, vs = O.quantize_kv_fp8(vx, d)
+    got = gpu_prefill(q, k8, v8, ks, vs, n, 0, hq, hkv, d, scale)
+    want = O.attention_f32(q, k8, v8, ks, vs, n, 0, hq, hkv, d, scale, NTHREADS)
+    a = O.bf16_to_f32(got).astype(np.float64) / mag
+    b = O.bf16_to_f32(want).astype(np.float64) / mag
+    assert np.isfinite(a).all()
+    err = np.abs(a - b)
+    assert err.max() <= MAX_ABS and err.mean() <= MEAN_ABS, (err.max(), err.mean())
