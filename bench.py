@@ -71,6 +71,7 @@ def graph_us(torch, stream, fn, iters):
     timed over a replay (one warm replay first): the kernels back to back,
     without the host launch rate of an eager loop."""
     g = torch.cuda.CUDAGraph()
+    torch.cuda.synchronize()   # work queued on other streams lands first
     with torch.cuda.stream(stream):
         fn()
         torch.cuda.synchronize()
@@ -98,6 +99,7 @@ def bench_decode(torch, R, args, stream):
     backend = R.AdaptiveAttention(R.AttnConfig(hq, hkv, d, scale))
     pos = torch.zeros(1, dtype=torch.int32, device=dev)
     chunk = 4096
+    torch.cuda.synchronize()   # the allocations above are initialized on the default stream
     with torch.cuda.stream(stream):
         for l in range(L):
             for s0 in range(0, depth, chunk):
@@ -202,6 +204,7 @@ def bench_prefill(torch, R, stream, n=4096, iters=None):
     gen.manual_seed(4321)
     cache = R.KVCache(1, n, hkv, d, device=dev)
     pos = torch.zeros(1, dtype=torch.int32, device=dev)
+    torch.cuda.synchronize()   # pos is written on the default stream
     with torch.cuda.stream(stream):
         q = torch.randn((n, hq, d), generator=gen, device=dev).to(torch.bfloat16)
         k = torch.randn((n, hkv, d), generator=gen, device=dev).to(torch.bfloat16)
@@ -247,6 +250,7 @@ def bench_rope_append(torch, R, stream, n=4096, iters=20):
     positions = torch.arange(n, dtype=torch.int32, device=dev)
     inv = (1e6 ** (-torch.arange(0, d, 2, dtype=torch.float64, device=dev) / d)).float()
     eps = 1e-6
+    torch.cuda.synchronize()   # pos, positions, inv are written on the default stream
     with torch.cuda.stream(stream):
         q = torch.randn((n, hq, d), generator=gen, device=dev).to(torch.bfloat16)
         k = torch.randn((n, hkv, d), generator=gen, device=dev).to(torch.bfloat16)
@@ -302,6 +306,7 @@ def decode_kernel_sweep(torch, R, stream, points, quiet=False):
         out = torch.empty((L, hq, d), dtype=torch.bfloat16, device=dev)
         pos = torch.full((1,), ctx - 1, dtype=torch.int32, device=dev)
         n = L * max(2, math.ceil(200 / L))
+        torch.cuda.synchronize()   # the fills above run on the default stream
         with torch.cuda.stream(stream):
             g = torch.cuda.CUDAGraph()
             with torch.cuda.graph(g, stream=stream):
@@ -368,6 +373,7 @@ def eager_kernels(torch, R, stream, args):
     kn = torch.randn((L, hkv, d), device=dev).to(torch.bfloat16)
     out = torch.empty((L, hq, d), dtype=torch.bfloat16, device=dev)
     pos = torch.full((1,), ctx - 1, dtype=torch.int32, device=dev)
+    torch.cuda.synchronize()   # the fills above run on the default stream
     with torch.cuda.stream(stream):
         for i in range(2 * L):
             l = i % L
