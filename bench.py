@@ -359,8 +359,9 @@ def copy_calibration(torch, stream):
 def eager_kernels(torch, R, stream, args):
     """The bench's kernels launched eagerly (no graph) so a profiler attributes
     counters per dispatch: 56 decode calls at ctx args.ctx rotating over 28
-    layers (24Q/8KV), 28 one-token appends, and 3 prefill calls at 4096."""
-    hq, hkv, d, L = 24, 8, 128, 28
+    layers (args.hq q heads / 8 kv heads, args.splits splits), 28 one-token
+    appends, and 3 prefill calls at 4096."""
+    hq, hkv, d, L = args.hq, 8, 128, 28
     ctx = args.ctx
     dev = torch.device("cuda:0")
     cache = R.KVCache(L, ctx, hkv, d, device=dev)
@@ -368,7 +369,8 @@ def eager_kernels(torch, R, stream, args):
     cache.v.random_(0, 126)
     cache.k_scale.uniform_(0.001, 0.01)
     cache.v_scale.uniform_(0.001, 0.01)
-    backend = R.AdaptiveAttention(R.AttnConfig(hq, hkv, d, 1.0 / math.sqrt(d)))
+    backend = R.AdaptiveAttention(R.AttnConfig(hq, hkv, d, 1.0 / math.sqrt(d)),
+                                  num_splits=args.splits)
     q = torch.randn((L, hq, d), device=dev).to(torch.bfloat16)
     kn = torch.randn((L, hkv, d), device=dev).to(torch.bfloat16)
     out = torch.empty((L, hq, d), dtype=torch.bfloat16, device=dev)
@@ -501,7 +503,13 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=128)
     ap.add_argument("--ctx", type=int, default=8196)
     ap.add_argument("--prefill-n", type=int, default=4096)
+    ap.add_argument("--hq", type=int, default=24, help="--mode kernels: q heads of the decode")
+    ap.add_argument("--splits", type=int, default=None,
+                    help="--mode kernels: decode split count (default: the backend's)")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--decode-kernel", choices=("auto", "valu"), default="auto",
+                    help="valu: run every decode call on the VALU split kernel (A/B against "
+                         "the MFMA kernel with --mode kernels or --sweep decode)")
     ap.add_argument("--sweep", nargs="?", const="all", choices=("all", "decode", "prefill"),
                     help="per-call decode and/or prefill sweeps over the BASELINE depths")
     ap.add_argument("--mode", choices=("full", "kernels", "copy"), default="full",
@@ -518,6 +526,8 @@ def main() -> int:
     import runtherder_amd as R
 
     R._ffi.load()
+    if args.decode_kernel == "valu":
+        R.set_decode_kernel(R.DECODE_VALU)
     stream = torch.cuda.Stream()
     torch.cuda.synchronize()
     if args.mode == "copy":

@@ -100,6 +100,14 @@ enum {
  * supported. Lets a caller or a test tell the two paths apart. */
 int rth_decode_path(int num_q_heads, int num_kv_heads, int head_dim);
 
+/* No counterpart in the reference: process-wide choice of the split kernel
+ * for the non-paged decode entries, for measurement and tuning. path 0 (the
+ * default) = the MFMA kernel wherever it supports the shape, the VALU kernel
+ * elsewhere; RTH_DECODE_VALU = the VALU kernel for every shape. Results of
+ * the two kernels agree within the attention tolerance, not bit for bit.
+ * Not synchronized with calls in flight on other host threads. */
+int rth_set_decode_kernel(int path);
+
 /* No counterpart in the reference: rth_attn_decode_split without the
  * `partial` argument, for callers that cannot allocate (code under HIP graph
  * capture, tight serving loops, harnesses that forbid hipMalloc). It calls no

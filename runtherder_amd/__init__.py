@@ -21,6 +21,7 @@ from .ops import (  # noqa: F401
     DECODE_MFMA,
     DECODE_VALU,
     decode_path,
+    set_decode_kernel,
     default_num_splits,
     flash_decode_append_split_bf16,
     flash_decode_split_bf16,

@@ -24,6 +24,7 @@ _SIGNATURES = {
     "rth_attn_decode_split": (_c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_int, _vp,
                                        _c_int, _c_int, _c_int, ctypes.c_float, _vp]),
     "rth_decode_path": (_c_int, [_c_int, _c_int, _c_int]),
+    "rth_set_decode_kernel": (_c_int, [_c_int]),
     "rth_attn_decode_split_noalloc": (_c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _c_int, _vp,
                                                _c_int, _c_int, _c_int, ctypes.c_float, _vp]),
     "rth_attn_decode_append_split": (_c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,

@@ -120,6 +120,16 @@ int block_shift_of(int block_size) {
     return sh;
 }
 
+// Process-wide decode kernel choice (rth_set_decode_kernel): 0 = the MFMA
+// split kernel wherever it supports the shape, RTH_DECODE_VALU = the VALU
+// split kernel for every non-paged decode call.
+std::atomic<int> g_decode_override{0};
+
+bool use_mfma_decode(int num_q_heads, int num_kv_heads, int head_dim) {
+    return g_decode_override.load(std::memory_order_relaxed) != RTH_DECODE_VALU &&
+           rth::decode_mfma_supported(num_q_heads, num_kv_heads, head_dim);
+}
+
 #define RTH_PAGED_ARGS(bt, bs, shift)                                              \
     RTH_REQUIRE((bt) != nullptr, "block_table must not be null");                  \
     const int shift = block_shift_of(bs);                                          \
@@ -213,7 +223,7 @@ int rth_attn_decode_split(uint16_t* out, const uint16_t* q, const uint8_t* k,
     RTH_REQUIRE(head_dim == 32 || head_dim == 64 || head_dim == 128 || head_dim == 256 ||
                     head_dim == 512,
                 "head_dim must be one of 32, 64, 128, 256, 512");
-    if (rth::decode_mfma_supported(num_q_heads, num_kv_heads, head_dim)) {
+    if (use_mfma_decode(num_q_heads, num_kv_heads, head_dim)) {
         RTH_REQUIRE(partial != nullptr, "partial must not be null");
         return check_hip(rth::flash_decode_launch(out, q, k, v, k_scale, v_scale, partial,
                                                   num_splits, cache_len, num_q_heads,
@@ -237,8 +247,16 @@ int rth_decode_path(int num_q_heads, int num_kv_heads, int head_dim) {
         head_dim != 512) {
         return 0;
     }
-    return rth::decode_mfma_supported(num_q_heads, num_kv_heads, head_dim) ? RTH_DECODE_MFMA
-                                                                           : RTH_DECODE_VALU;
+    return use_mfma_decode(num_q_heads, num_kv_heads, head_dim) ? RTH_DECODE_MFMA
+                                                                : RTH_DECODE_VALU;
+}
+
+int rth_set_decode_kernel(int path) {
+    RTH_REQUIRE(path == 0 || path == RTH_DECODE_VALU,
+                "rth_set_decode_kernel: path must be 0 (automatic) or RTH_DECODE_VALU");
+    g_decode_override.store(path, std::memory_order_relaxed);
+    g_last_error.clear();
+    return RTH_OK;
 }
 
 int rth_attn_decode_split_noalloc(uint16_t* out, const uint16_t* q, const uint8_t* k,
@@ -265,7 +283,7 @@ int rth_attn_decode_split_noalloc(uint16_t* out, const uint16_t* q, const uint8_
     if (int rc = check_hip(rth::noalloc_scratch(&partial), "rth_attn_decode_split_noalloc")) {
         return rc;
     }
-    if (!rth::decode_mfma_supported(num_q_heads, num_kv_heads, head_dim)) {
+    if (!use_mfma_decode(num_q_heads, num_kv_heads, head_dim)) {
         return check_hip(rth::flash_decode_valu_launch(out, q, k, v, k_scale, v_scale, partial,
                                                        num_splits, cache_len, num_q_heads,
                                                        num_kv_heads, head_dim, scale,
@@ -295,7 +313,7 @@ int rth_attn_decode_append_split(uint16_t* out, const uint16_t* q, uint8_t* k_ca
     RTH_REQUIRE(head_dim == 32 || head_dim == 64 || head_dim == 128 || head_dim == 256 ||
                     head_dim == 512,
                 "head_dim must be one of 32, 64, 128, 256, 512");
-    if (rth::decode_mfma_supported(num_q_heads, num_kv_heads, head_dim)) {
+    if (use_mfma_decode(num_q_heads, num_kv_heads, head_dim)) {
         RTH_REQUIRE(partial != nullptr, "partial must not be null");
         return check_hip(rth::flash_decode_launch(out, q, k_cache, v_cache, k_scale, v_scale,
                                                   partial, num_splits, cache_len, num_q_heads,

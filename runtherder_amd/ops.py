@@ -96,6 +96,13 @@ def decode_path(num_q_heads: int, num_kv_heads: int, head_dim: int) -> int:
     return int(_ffi.load().rth_decode_path(num_q_heads, num_kv_heads, head_dim))
 
 
+def set_decode_kernel(path: int) -> None:
+    """Process-wide split-kernel choice for the non-paged decode entries: 0
+    (automatic: MFMA where supported) or DECODE_VALU (the VALU kernel for
+    every shape), for measurement. No reference counterpart."""
+    _ffi.call("rth_set_decode_kernel", int(path))
+
+
 def flash_decode_split_bf16_noalloc(out, q, k, v, k_scale, v_scale, num_splits, cache_len,
                                     num_q_heads, num_kv_heads, head_dim, scale, stream=None):
     """flash_decode_split_bf16 without caller scratch (no reference

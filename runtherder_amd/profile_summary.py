@@ -3,6 +3,11 @@ markdown, for the text files kept under profiles/.
 
   python -m runtherder_amd.profile_summary stats <rocprof_dir>
   python -m runtherder_amd.profile_summary pmc <rocprof_dir> [kernel-substring]
+  python -m runtherder_amd.profile_summary loop <rocprof_dir> <after-substring> <kernel-substring> <count>
+
+"loop": mean tracer durations of the first <count> dispatches matching
+<kernel-substring> that follow the last dispatch matching <after-substring>,
+and of the dispatch right after each (e.g. a split kernel and its merge).
 """
 from __future__ import annotations
 
@@ -42,6 +47,31 @@ def pmc(root: str, pattern: str = "") -> dict[str, dict[str, float]]:
     return {k: {c: sum(v) / len(v) for c, v in cs.items()} for k, cs in acc.items()}
 
 
+def loop(root: str, after: str, kernel: str, count: int) -> str:
+    rows = []
+    for f in glob.glob(f"{root}/**/*kernel_trace.csv", recursive=True):
+        rows += list(csv.DictReader(open(f)))
+    rows.sort(key=lambda r: int(r["Start_Timestamp"]))
+    dur = [int(r["End_Timestamp"]) - int(r["Start_Timestamp"]) for r in rows]
+    start = max((i for i, r in enumerate(rows) if after in r["Kernel_Name"]), default=-1) + 1
+    first, second, names = [], [], None
+    i = start
+    while len(first) < count and i + 1 < len(rows):
+        if kernel in rows[i]["Kernel_Name"]:
+            first.append(dur[i])
+            second.append(dur[i + 1])
+            names = (_short(rows[i]["Kernel_Name"]), _short(rows[i + 1]["Kernel_Name"]))
+            i += 2
+        else:
+            i += 1
+    if not first:
+        return "no matching dispatches"
+    mean = lambda v: sum(v) / len(v) / 1e3
+    return (f"| dispatches | {names[0]} avg us | {names[1]} avg us | sum us |\n|---|---|---|---|\n"
+            f"| {len(first)} | {mean(first):.2f} | {mean(second):.2f} | "
+            f"{mean(first) + mean(second):.2f} |")
+
+
 def main(argv: list[str]) -> int:
     if len(argv) >= 2 and argv[0] == "stats":
         print(stats(argv[1]))
@@ -52,6 +82,9 @@ def main(argv: list[str]) -> int:
         for k, cs in res.items():
             for c, v in sorted(cs.items()):
                 print(f"| {k} | {c} | {v:.6g} |")
+        return 0
+    if len(argv) >= 5 and argv[0] == "loop":
+        print(loop(argv[1], argv[2], argv[3], int(argv[4])))
         return 0
     print(__doc__)
     return 2

@@ -283,3 +283,21 @@ def test_decode_append_fused(cache_len, hq, hkv, d, splits):
     two = gpu_decode(q, gk, gv, gks, gvs, cache_len, hq, hkv, d, splits, scale)
     mx, mean = O.bf16_err(got, two)
     assert mx <= MAX_ABS and mean <= 1e-3, (mx, mean)
+
+
+def test_forced_valu_kernel_matches_oracle():
+    """rth_set_decode_kernel(RTH_DECODE_VALU) runs the VALU split kernel for
+    a shape the MFMA kernel serves (the A/B switch of the measurements);
+    results stay within the attention tolerance, and the default returns."""
+    hq, hkv, d, ctx = 24, 8, 128, 8196
+    scale = np.float32(1.0 / np.sqrt(d))
+    q = O.normal_bf16((hq, d), 95)
+    _, _, k8, v8, ks, vs = make_cache(ctx, hkv, d, kind="normal", seed=95)
+    R.set_decode_kernel(R.DECODE_VALU)
+    try:
+        assert R.decode_path(hq, hkv, d) == R.DECODE_VALU
+        got = gpu_decode(q, k8, v8, ks, vs, ctx - 1, hq, hkv, d, 256, scale)
+    finally:
+        R.set_decode_kernel(0)
+    assert R.decode_path(hq, hkv, d) == R.DECODE_MFMA
+    check(got, q, k8, v8, ks, vs, ctx - 1, hq, hkv, d, scale)
