@@ -57,7 +57,8 @@ constexpr int kMaxGroupD  = 2048;   // G * head_dim bound of a wave's LDS partia
 constexpr int kCombineThreads = 128;
 constexpr int kCombineSlice   = 16;    // head_dim slice per merge workgroup
 constexpr int kCoopMaxKeys    = 4096;  // contexts up to this run cooperative workgroups
-constexpr int kNtMinTiles     = 8;     // tiles past the first a wave streams with nontemporal loads
+constexpr int kNtMinTiles     = 2;     // tiles past the first a wave streams with nontemporal loads
+constexpr int kValuNtMinSteps = 32;    // VALU kernel: steps above which its loads are nontemporal
 
 template <int D>
 struct DecTraits {
@@ -104,27 +105,45 @@ __device__ __forceinline__ T ld(const T* p) {
     }
 }
 
-// Loads one tile's codes and scales. kNT: the K/V codes (read exactly once
-// per call) use nontemporal loads, which stream faster once a wave has many
-// tiles to read but have a longer latency than plain loads.
+// Chunk swizzle of a wave's LDS K tile (32 rows of D bytes): row r keeps
+// its 16-byte chunk c at position c ^ k_swz(r), so that the MFMA-layout reads
+// (16 lanes = 16 rows x one chunk) hit 16 distinct 4-bank groups.
+template <int D>
+__device__ __forceinline__ int k_swz(int r) {
+    return (r / (256 / D)) & (D / 16 - 1);
+}
+
+// Loads one tile's codes and scales. The K codes are read as whole rows:
+// each load instruction covers 1024 / D complete D-byte rows (D / 16 lanes
+// per row), which streams faster than loading the MFMA layout directly (16
+// half rows per instruction; a read probe of the two access patterns at 128K
+// keys x 8 kv heads: 6.3 vs 5.7 TB/s). The lane of row r, position c loads
+// chunk c ^ k_swz(r); k_rows_to_mfma moves the tile into the MFMA layout
+// through LDS. V rows are read 16 lanes x kVBytes per key (whole rows
+// already), the scales one per lane. kNT: the K/V codes (read exactly once
+// per call) use nontemporal loads, which stream faster once a wave has
+// several tiles to read but have a longer latency than plain loads.
 template <int D, bool kNT>
 __device__ __forceinline__ void load_tile(TileRaw<D>& t, const uint8_t* __restrict__ k,
-                                          const uint8_t* __restrict__ v,
-                                          const float* __restrict__ ks,
-                                          const float* __restrict__ vs, int kb,
-                                          int k1, int kvh, int hkv, int lane, int delta) {
-    using T     = DecTraits<D>;
+                                               const uint8_t* __restrict__ v,
+                                               const float* __restrict__ ks,
+                                               const float* __restrict__ vs, int kb, int k1,
+                                               int kvh, int hkv, int lane, int delta) {
+    using T             = DecTraits<D>;
+    constexpr int kCpr  = D / 16;          // 16-byte chunks per row
+    constexpr int kRpi  = kWave / kCpr;    // rows per load instruction
+    const int     rr    = lane / kCpr;
+    const int     ch    = lane % kCpr;
+#pragma unroll
+    for (int i = 0; i < kTileKeys / kRpi; ++i) {
+        const int      r   = i * kRpi + rr;
+        const int      key = min(kb + r, k1 - 1);
+        const uint8_t* kr  = k + (static_cast<int64_t>(key + delta) * hkv + kvh) * D;
+        t.kraw[i / T::kKChunks][i % T::kKChunks] =
+            ld<kNT>(reinterpret_cast<const u32x4*>(kr + 16 * (ch ^ k_swz<D>(r))));
+    }
     const int n = lane & 15;
     const int g = lane >> 4;
-#pragma unroll
-    for (int u = 0; u < 2; ++u) {
-        const int      key = min(kb + 16 * u + n, k1 - 1);
-        const uint8_t* kr  = k + (static_cast<int64_t>(key + delta) * hkv + kvh) * D;
-#pragma unroll
-        for (int c = 0; c < T::kKChunks; ++c) {
-            t.kraw[u][c] = ld<kNT>(reinterpret_cast<const u32x4*>(kr + 16 * g + 64 * c));
-        }
-    }
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
         const int      key = min(kb + key_of(g, j), k1 - 1);
@@ -147,6 +166,32 @@ __device__ __forceinline__ void load_tile(TileRaw<D>& t, const uint8_t* __restri
         const int     key = min(kb + (lane & 31), k1 - 1);
         const int64_t row = static_cast<int64_t>(key + delta) * hkv + kvh;
         t.sc              = (lane < 32) ? ks[row] : vs[row];
+    }
+}
+
+// Rewrites the K registers of a load_tile tile into the MFMA layout
+// (lane (n, g) holds bytes 16g + 64c of row 16u + n in kraw[u][c])
+// through buf, D * 32 bytes of this wave's LDS: the tile is stored as loaded
+// (slot lane + 64i) and read back by rows. LDS operations of one wave run in
+// order, so no wait separates the stores from the loads.
+template <int D>
+__device__ __forceinline__ void k_rows_to_mfma(TileRaw<D>& t, uint8_t* buf, int lane) {
+    using T = DecTraits<D>;
+#pragma unroll
+    for (int i = 0; i < D / 32; ++i) {
+        *reinterpret_cast<u32x4*>(buf + 16 * (lane + kWave * i)) =
+            t.kraw[i / T::kKChunks][i % T::kKChunks];
+    }
+    const int n = lane & 15;
+    const int g = lane >> 4;
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+#pragma unroll
+        for (int c = 0; c < T::kKChunks; ++c) {
+            const int r  = 16 * u + n;
+            t.kraw[u][c] = *reinterpret_cast<const u32x4*>(buf + r * D +
+                                                           16 * ((4 * c + g) ^ k_swz<D>(r)));
+        }
     }
 }
 
@@ -227,7 +272,8 @@ __host__ __device__ constexpr int dec_workgroups(int num_splits, int hkv, int kv
 }
 
 // The appended token's quantized K/V codes for one (kv head) unit, laid out
-// as the tile registers of key 0 of a tile (see load_tile) plus the scales.
+// as the tile registers of key 0 of a tile after k_rows_to_mfma, plus the
+// scales.
 template <int D>
 __device__ __forceinline__ void quantize_new_token(TileRaw<D>& vt, const uint16_t* __restrict__ kx,
                                                    const uint16_t* __restrict__ vx,
@@ -393,8 +439,13 @@ __global__ __launch_bounds__(kDecThreads) void flash_decode_kernel(
     const bool virt    = owner && (!pt.coop || wave >= kDecWaves - pt.gkv);
     const int  k1      = owner ? p_new : min(split_tile(pt, si + 1) * kTileKeys, n_keys);
     const int  n_tiles = (k1 - k0 + kTileKeys - 1) / kTileKeys;
-    const int  t_first = pt.coop ? wave / pt.gkv : 0;
-    const int  t_step  = pt.coop ? wpk : 1;
+    // Tiles [t_first, last_tile] of the split: all of them for a solo wave;
+    // in coop mode wave j of its kv head's wpk waves takes a contiguous
+    // share (floor(j n / wpk) .. floor((j + 1) n / wpk) - 1).
+    const int  wj        = pt.coop ? wave / pt.gkv : 0;
+    const int  wn        = pt.coop ? wpk : 1;
+    const int  t_first   = (wj * n_tiles) / wn;
+    const int  last_tile = ((wj + 1) * n_tiles) / wn - 1;
 
     // Q^T as the B operand: column n = q head of the group (zero past G).
     bf16x8 qop[T::kKSteps];
@@ -525,7 +576,6 @@ __global__ __launch_bounds__(kDecThreads) void flash_decode_kernel(
     // flight per wave while it computes. Tile indices past this wave's last
     // tile are clamped to it; those reloads hit in L2 and are never consumed.
     constexpr int kRing     = DecTraits<D>::kRing;
-    const int     last_tile = n_tiles - 1;
     if (t_first <= last_tile) {
         auto tile_delta = [&](int kb) {
             if constexpr (kPaged) {
@@ -534,24 +584,28 @@ __global__ __launch_bounds__(kDecThreads) void flash_decode_kernel(
                 return 0;
             }
         };
+        // The wave's own sm_o row is free until the partial is written.
+        uint8_t* kbuf = reinterpret_cast<uint8_t*>(sm_o[wave]);
         auto stream = [&]<bool kNT>() {
+            auto load = [&](TileRaw<D>& t, int kb) {
+                load_tile<D, kNT>(t, k, v, ks, vs, kb, k1, kvh, hkv, lane, tile_delta(kb));
+            };
             TileRaw<D> ring[kRing];
 #pragma unroll
             for (int r = 0; r + 1 < kRing; ++r) {
-                const int kb = k0 + min(t_first + r * t_step, last_tile) * kTileKeys;
-                load_tile<D, kNT>(ring[r], k, v, ks, vs, kb, k1, kvh, hkv, lane, tile_delta(kb));
+                load(ring[r], k0 + min(t_first + r, last_tile) * kTileKeys);
             }
-            for (int t = t_first;; t += kRing * t_step) {
+            for (int t = t_first;; t += kRing) {
                 bool done = false;
 #pragma unroll
                 for (int r = 0; r < kRing; ++r) {
                     if (!done) {
-                        const int tr  = t + r * t_step;
-                        const int kbn = k0 + min(tr + (kRing - 1) * t_step, last_tile) * kTileKeys;
-                        load_tile<D, kNT>(ring[(r + kRing - 1) % kRing], k, v, ks, vs, kbn, k1,
-                                          kvh, hkv, lane, tile_delta(kbn));
+                        const int tr  = t + r;
+                        const int kbn = k0 + min(tr + kRing - 1, last_tile) * kTileKeys;
+                        load(ring[(r + kRing - 1) % kRing], kbn);
+                        k_rows_to_mfma<D>(ring[r], kbuf, lane);
                         process(ring[r], k0 + tr * kTileKeys, k1);
-                        done = tr + t_step > last_tile;
+                        done = tr + 1 > last_tile;
                     }
                 }
                 if (done) {
@@ -559,12 +613,13 @@ __global__ __launch_bounds__(kDecThreads) void flash_decode_kernel(
                 }
             }
         };
-        // A wave that streams many tiles (long splits) is bandwidth-bound:
-        // nontemporal loads. Short runs and the one-kv-head cooperative
-        // workgroups are latency-bound: plain loads (measured: 128K at 256
-        // splits 56.3 -> 51.8 us with nontemporal loads; 8K at 256 splits
-        // and 128K at 64 one-kv-head cooperative splits 6-8 % slower with
-        // them; 128K at 64 splits in two-kv-head workgroups 0.5 us faster).
+        // A wave that streams three or more tiles is bandwidth-bound:
+        // nontemporal loads. One- and two-tile runs (8K at 256 splits) and
+        // the one-kv-head cooperative workgroups are latency-bound: plain
+        // loads (measured: 128K at 256 splits 56.3 -> 51.8 us with
+        // nontemporal loads, 32K at 256 splits (4 tiles per wave) 20.5 ->
+        // 19.5 us; 8K at 256 splits and 128K at 64 one-kv-head cooperative
+        // splits 6-8 % slower with them).
         if ((!pt.coop || pt.gkv > 1) && last_tile - t_first >= kNtMinTiles) {
             stream.template operator()<true>();
         } else {
@@ -1021,7 +1076,7 @@ __global__ __launch_bounds__(kDecThreads) void flash_decode_valu_kernel(
                 }
             }
         };
-        if (n_steps > 4 * kNtMinTiles) {
+        if (n_steps > kValuNtMinSteps) {
             stream.template operator()<true>();
         } else {
             stream.template operator()<false>();
