@@ -585,6 +585,7 @@ __global__ __launch_bounds__(kDecThreads) void flash_decode_kernel(
             }
         };
         // The wave's own sm_o row is free until the partial is written.
+        static_assert(kMaxGroupD * sizeof(float) >= kTileKeys * D, "K tile fits in an sm_o row");
         uint8_t* kbuf = reinterpret_cast<uint8_t*>(sm_o[wave]);
         auto stream = [&]<bool kNT>() {
             auto load = [&](TileRaw<D>& t, int kb) {
