@@ -12,26 +12,23 @@
 //    O^T += V^T P^T. E4M3 codes convert exactly to bf16 in registers
 //    (v_cvt_scalef32_pk_bf16_fp8); the per-(token, kv_head) scales are folded
 //    in fp32 into the score column (k_scale) and into P (v_scale).
-//  * K is loaded with 16-byte lane loads along head_dim; V is loaded 8 bytes
-//    per (key, lane) and transposed in registers with v_perm so P^T needs no
-//    cross-lane movement. Each wave keeps a ring of two register tiles in
+//  * K is loaded as whole rows (16 bytes per lane) and moved into the MFMA
+//    layout through the wave's LDS; V is loaded 8 bytes per (key, lane) and
+//    transposed in registers with v_perm so P^T needs no cross-lane
+//    movement. Each wave keeps a ring of two register tiles in
 //    flight.
 //  * Softmax runs in base 2 (scores pre-multiplied by scale*log2(e)); the
 //    running-max rescale of the accumulator is skipped when no lane's max
 //    moved.
 //  * Partitions (see DecPartition):
-//      - num_splits * Hkv >= 8 * CUs units, long contexts (> kCoopMaxKeys
-//        keys): one WAVE per (kv head, split) unit. A workgroup holds the kv
-//        heads of one split (its waves share the interleaved scale lines in
-//        L1); waves never wait for each other and each writes its own
-//        partial.
-//      - the same launch at short contexts: one WORKGROUP per (kv head,
-//        split) over 8x fewer splits, the eight waves take alternate tiles
-//        and merge in LDS (the merge kernel's loads dominate at this size).
+//      - num_splits * Hkv >= 8 * CUs units: one WAVE per (kv head, split)
+//        unit. A workgroup holds the kv heads of one split (its waves share
+//        the interleaved scale lines in L1); waves never wait for each
+//        other and each writes its own partial.
 //      - fewer units (e.g. 64 splits x 8 kv heads): one workgroup per
 //        (group of kv heads, split), sized so the grid fills the chip; the
-//        waves of one kv head take alternate tiles and merge in LDS.
-//        Workgroups of one split land on one XCD.
+//        waves of one kv head take contiguous shares of the split's tiles
+//        and merge in LDS. Workgroups of one split land on one XCD.
 //  * A second small kernel merges the splits of every (q head, 16-wide d
 //    slice): one round of loads issued before *cache_len is known, an
 //    online max per thread over a strided subset of splits, lane exchanges,
@@ -56,7 +53,6 @@ constexpr int kTileKeys   = 32;     // keys per wave iteration (two 16-key MFMAs
 constexpr int kMaxGroupD  = 2048;   // G * head_dim bound of a wave's LDS partial staging
 constexpr int kCombineThreads = 128;
 constexpr int kCombineSlice   = 16;    // head_dim slice per merge workgroup
-constexpr int kCoopMaxKeys    = 4096;  // contexts up to this run cooperative workgroups
 constexpr int kNtMinTiles     = 2;     // tiles past the first a wave streams with nontemporal loads
 constexpr int kValuNtMinSteps = 32;    // VALU kernel: steps above which its loads are nontemporal
 
@@ -198,16 +194,16 @@ __device__ __forceinline__ void k_rows_to_mfma(TileRaw<D>& t, uint8_t* buf, int 
 // Partition of the decode work for one call. With fewer units than one
 // round of wave slots (num_splits * hkv < 8 * CUs) the host launches one
 // workgroup per (group of kvg kv heads, split): the workgroup's waves are kvg kv heads x
-// 8 / kvg waves per kv head, the waves of one kv head take alternate tiles of
-// the split and merge in LDS ("coop"); kvg is chosen so the grid still fills
+// 8 / kvg waves per kv head, the waves of one kv head take contiguous shares
+// of the split's tiles and merge in LDS ("coop"); kvg is chosen so the grid still fills
 // the chip (more kv heads per workgroup read longer runs of each interleaved
-// [token, kv_head] row). Otherwise it launches one wave per unit, eight per
-// workgroup (kvg = 0); then long contexts run one wave per (kv head, split)
-// unit (num_splits splits, no merge inside a workgroup) and contexts up to
-// kCoopMaxKeys switch to coop with one kv head per workgroup over n_wgs / hkv
-// splits, which leaves 8x fewer partials for the merge kernel. Both kernels
-// derive the same partition from *cache_len and the launch shape, so it is
-// decided on device per call.
+// [token, kv_head] row). Otherwise (kvg = 0, and always in the VALU kernel)
+// it launches one wave per (kv head, split) unit, eight per workgroup, with
+// no merge inside a workgroup. (Cooperative workgroups over 8x fewer splits
+// at short contexts, which leave 8x fewer partials for the merge kernel,
+// measured 1.1-1.5 us per call slower than one wave per unit from 35 to
+// 16384 keys.) Both kernels derive the same split bounds from *cache_len and
+// kvg, so they are decided on device per call.
 //
 // The key range is cut into kTileKeys-key tiles dealt out evenly: split si
 // holds tiles [split_tile(si), split_tile(si + 1)), floor or ceil of
@@ -228,23 +224,11 @@ __device__ __forceinline__ int split_tile(const DecPartition& pt, int si) {
     return si * pt.base + min(si, pt.rem);
 }
 
-__device__ __forceinline__ DecPartition dec_partition(int n_keys, int num_splits, int hkv,
-                                                      int n_wgs, int kvg) {
+__device__ __forceinline__ DecPartition dec_partition(int n_keys, int num_splits, int kvg) {
     DecPartition pt;
-    if (kvg > 0) {
-        pt.coop   = true;
-        pt.splits = num_splits;
-        pt.gkv    = kvg;
-    } else if (kvg < 0) {   // the VALU kernel: one wave per unit at every context
-        pt.coop   = false;
-        pt.splits = num_splits;
-        pt.gkv    = 1;
-    } else {
-        const int coop_splits = n_wgs / hkv;
-        pt.coop               = (n_keys <= kCoopMaxKeys) && (coop_splits >= 1);
-        pt.splits             = pt.coop ? coop_splits : num_splits;
-        pt.gkv                = 1;
-    }
+    pt.coop   = kvg > 0;
+    pt.splits = num_splits;
+    pt.gkv    = pt.coop ? kvg : 1;
     const int tiles = (n_keys + kTileKeys - 1) / kTileKeys;
     pt.n_eff        = min(pt.splits, tiles);
     pt.base         = tiles / pt.n_eff;
@@ -399,10 +383,9 @@ __global__ __launch_bounds__(kDecThreads) void flash_decode_kernel(
     const int bid  = static_cast<int>(blockIdx.x);
 
     const int          n_keys = *cache_len + 1;
-    const DecPartition pt     = dec_partition(n_keys, num_splits, hkv,
-                                              static_cast<int>(gridDim.x), kvg);
+    const DecPartition pt     = dec_partition(n_keys, num_splits, kvg);
     // coop: workgroup = (group of gkv kv heads, split); wave w serves kv head
-    //       w % gkv of the group and takes tiles w / gkv, + 8 / gkv, ...
+    //       w % gkv of the group and share j = w / gkv of its tiles
     // solo: wave = (kv head, split) unit; adjacent units are the kv heads of
     //       one split, so a workgroup's waves share the scale lines in L1.
     int       kvh, si;
@@ -640,7 +623,7 @@ __global__ __launch_bounds__(kDecThreads) void flash_decode_kernel(
 
     // ---- partial of this split, reference layout: m at [h*S + si] (log2
     // units), l at [Hq*S + h*S + si], acc at [2*Hq*S + (h*S + si)*D + d]
-    // with S = num_splits (coop mode fills the first pt.splits slots).
+    // with S = num_splits.
     l_run = wave_xor_sum(l_run, 16);
     l_run = wave_xor_sum(l_run, 32);
     const int64_t hs     = static_cast<int64_t>(hq) * num_splits;
@@ -755,7 +738,7 @@ __global__ __launch_bounds__(kDecThreads) void flash_decode_kernel(
 template <int D>
 __global__ __launch_bounds__(kCombineThreads) void flash_decode_combine_kernel(
     uint16_t* __restrict__ out, const float* __restrict__ partial, int num_splits,
-    const int* __restrict__ cache_len, int hq, int hkv, int n_wgs, int kvg) {
+    const int* __restrict__ cache_len, int hq, int kvg) {
     constexpr int kQuads  = kCombineSlice / 4;
     constexpr int kGroups = kCombineThreads / kQuads;
     constexpr int kCWaves = kCombineThreads / kWave;
@@ -815,7 +798,7 @@ __global__ __launch_bounds__(kCombineThreads) void flash_decode_combine_kernel(
     };
     load8(grp, num_splits - 1);
     const int n_keys = *cache_len + 1;
-    const int n_eff  = dec_partition(n_keys, num_splits, hkv, n_wgs, kvg).n_eff;
+    const int n_eff  = dec_partition(n_keys, num_splits, kvg).n_eff;
     fold(grp, n_eff);
     for (int s0 = grp + 8 * kGroups; s0 < n_eff; s0 += 8 * kGroups) {
         load8(s0, n_eff - 1);
@@ -956,7 +939,7 @@ __global__ __launch_bounds__(kDecThreads) void flash_decode_valu_kernel(
     const int si   = unit / nb / hkv;
 
     const int          n_keys = *cache_len + 1;
-    const DecPartition pt     = dec_partition(n_keys, num_splits, hkv, 0, -1);
+    const DecPartition pt     = dec_partition(n_keys, num_splits, 0);
     if (si >= pt.n_eff) {
         return;
     }
@@ -1145,7 +1128,7 @@ hipError_t launch_decode_valu(uint16_t* out, const uint16_t* q, const uint8_t* k
     hipLaunchKernelGGL(flash_decode_combine_kernel<D>,
                        dim3(static_cast<unsigned>(hq), static_cast<unsigned>(D / kCombineSlice)),
                        dim3(kCombineThreads), 0, stream, out, partial, num_splits, cache_len,
-                       hq, hkv, 0, -1);
+                       hq, 0);
     return hipGetLastError();
 }
 
@@ -1189,7 +1172,7 @@ hipError_t launch_decode(uint16_t* out, const uint16_t* q, const uint8_t* k,
     hipLaunchKernelGGL(flash_decode_combine_kernel<D>,
                        dim3(static_cast<unsigned>(hq), static_cast<unsigned>(D / kCombineSlice)),
                        dim3(kCombineThreads), 0, stream, out, partial, num_splits,
-                       cache_len, hq, hkv, n_wgs, kvg);
+                       cache_len, hq, kvg);
     return hipGetLastError();
 }
 

@@ -160,7 +160,7 @@ def test_long_splits_ragged_tail():
 def test_grouped_workgroups(ctx, hq, hkv, splits):
     """Launches with fewer (kv head, split) units than one round of wave
     slots run one workgroup per (group of kv heads, split), the waves of a kv
-    head on alternate tiles, merged in LDS. On 256 compute units: 64 splits x
+    head on contiguous shares of the split's tiles, merged in LDS. On 256 compute units: 64 splits x
     8 kv heads -> 2 kv heads per workgroup, 128 x 8 -> 4, 16 x 8 -> 1,
     128 x 4 -> 2; short contexts leave most splits empty."""
     d = 128
