@@ -397,8 +397,10 @@ __global__ __launch_bounds__(kWaves * kWave, kSplit ? 1 : 2) void flash_prefill_
     // t = s * (k_scale * scale * log2 e) - m_ref (register r of block kb is key
     // 32kb + 8(r/4) + 4h + r%4 of the tile), the causal / key-end mask only on
     // tiles that cross the diagonal or the end of the keys (a wave-uniform
-    // branch), p = 2^t rounded to f16 and the row sum of those f16 values (four
-    // partial sums). Lazy reference maximum (exact): m_ref moves to the row
+    // branch), e = 2^t in fp32, p = e rounded to f16 for the P V MFMAs, and
+    // the row sum of the fp32 e (four partial sums of VALU adds, as the
+    // reference sums its fp32 exponentials; a v_dot2c sum of the f16 p runs on
+    // the MFMA pipe and measured ~1 % slower). Lazy reference maximum (exact): m_ref moves to the row
     // maximum only on a wave's first tile or when a row sum exceeds 2^15 (some
     // score more than 15 above m_ref); otherwise the tile needs no max
     // reduction, no cross-lane step and no rescale of l and O. Every p and l
@@ -448,11 +450,10 @@ __global__ __launch_bounds__(kWaves * kWave, kSplit ? 1 : 2) void flash_prefill_
 #pragma unroll
                     for (int i = 0; i < 4; ++i) {
                         const int   r  = 8 * half + 2 * i;
-                        const f16x2 pp = {
-                            static_cast<_Float16>(__builtin_amdgcn_exp2f(sx[kb][r])),
-                            static_cast<_Float16>(__builtin_amdgcn_exp2f(sx[kb][r + 1]))};
-                        part[i] = __builtin_amdgcn_fdot2(pp, f16x2{1.0f16, 1.0f16}, part[i],
-                                                         false);
+                        const float e0 = __builtin_amdgcn_exp2f(sx[kb][r]);
+                        const float e1 = __builtin_amdgcn_exp2f(sx[kb][r + 1]);
+                        const f16x2 pp = {static_cast<_Float16>(e0), static_cast<_Float16>(e1)};
+                        part[i] += e0 + e1;
                         pw[2 * i]     = pp.x;
                         pw[2 * i + 1] = pp.y;
                     }
