@@ -400,7 +400,8 @@ __global__ __launch_bounds__(kWaves * kWave, kSplit ? 1 : 2) void flash_prefill_
     // branch), e = 2^t in fp32, p = e rounded to f16 for the P V MFMAs, and
     // the row sum of the fp32 e (four partial sums of VALU adds, as the
     // reference sums its fp32 exponentials; a v_dot2c sum of the f16 p runs on
-    // the MFMA pipe and measured ~1 % slower). Lazy reference maximum (exact): m_ref moves to the row
+    // the MFMA pipe and measured ~1 % slower; the key-split kernel keeps that
+    // form for its register budget). Lazy reference maximum (exact): m_ref moves to the row
     // maximum only on a wave's first tile or when a row sum exceeds 2^15 (some
     // score more than 15 above m_ref); otherwise the tile needs no max
     // reduction, no cross-lane step and no rescale of l and O. Every p and l
@@ -453,7 +454,14 @@ __global__ __launch_bounds__(kWaves * kWave, kSplit ? 1 : 2) void flash_prefill_
                         const float e0 = __builtin_amdgcn_exp2f(sx[kb][r]);
                         const float e1 = __builtin_amdgcn_exp2f(sx[kb][r + 1]);
                         const f16x2 pp = {static_cast<_Float16>(e0), static_cast<_Float16>(e1)};
-                        part[i] += e0 + e1;
+                        if constexpr (kSplit) {
+                            // The key-split kernel sits at 256 VGPRs; the fp32
+                            // sum would spill there.
+                            part[i] = __builtin_amdgcn_fdot2(pp, f16x2{1.0f16, 1.0f16},
+                                                             part[i], false);
+                        } else {
+                            part[i] += e0 + e1;
+                        }
                         pw[2 * i]     = pp.x;
                         pw[2 * i + 1] = pp.y;
                     }
