@@ -153,17 +153,20 @@ def test_long_splits_ragged_tail():
     check(got, q, k8, v8, ks, vs, ctx - 1, hq, hkv, d, scale)
 
 
-@pytest.mark.parametrize("ctx,hq,hkv,splits", [
-    (20000, 32, 8, 64), (20001, 32, 8, 128), (7000, 32, 8, 16), (12345, 16, 4, 128),
-    (3000, 32, 8, 128), (33, 32, 8, 64),
+@pytest.mark.parametrize("ctx,hq,hkv,splits,d", [
+    (20000, 32, 8, 64, 128), (20001, 32, 8, 128, 128), (7000, 32, 8, 16, 128),
+    (12345, 16, 4, 128, 128), (3000, 32, 8, 128, 128), (33, 32, 8, 64, 128),
+    (20000, 32, 8, 64, 64), (9001, 16, 4, 128, 64), (20000, 32, 8, 64, 256),
+    (9001, 16, 4, 128, 256),
 ])
-def test_grouped_workgroups(ctx, hq, hkv, splits):
+def test_grouped_workgroups(ctx, hq, hkv, splits, d):
     """Launches with fewer (kv head, split) units than one round of wave
     slots run one workgroup per (group of kv heads, split), the waves of a kv
-    head on contiguous shares of the split's tiles, merged in LDS. On 256 compute units: 64 splits x
-    8 kv heads -> 2 kv heads per workgroup, 128 x 8 -> 4, 16 x 8 -> 1,
-    128 x 4 -> 2; short contexts leave most splits empty."""
-    d = 128
+    head on contiguous shares of the split's tiles, merged in LDS. On 256
+    compute units: 64 splits x 8 kv heads -> 2 kv heads per workgroup,
+    128 x 8 -> 4, 16 x 8 -> 1, 128 x 4 -> 2; short contexts leave most splits
+    empty. head_dim 64 and 256 cover the other whole-row K layouts (16 and 4
+    rows per load instruction; 256 with its one-tile register ring)."""
     scale = np.float32(1.0 / np.sqrt(d))
     q = O.normal_bf16((hq, d), 81)
     _, _, k8, v8, ks, vs = make_cache(ctx, hkv, d, kind="normal", seed=ctx)

@@ -82,10 +82,17 @@ def test_paged_append_bytes(total, block):
     assert np.array_equal(gvs.view(np.uint32), cont.v_scale[0].cpu().numpy()[:total].view(np.uint32))
 
 
-@pytest.mark.parametrize("total,block,splits", [(35, 32, None), (2041, 64, None), (8196, 128, None),
-                                                (5000, 32, 64), (300, 64, 7)])
-def test_paged_decode_equals_contiguous(total, block, splits):
-    hq, hkv, d = 24, 8, 128
+@pytest.mark.parametrize("total,block,splits,d", [
+    (35, 32, None, 128), (2041, 64, None, 128), (8196, 128, None, 128), (5000, 32, 64, 128),
+    (300, 64, 7, 128),
+    # long per-wave streams (nontemporal loads, the paged reload past a wave's
+    # last tile): grouped workgroups at 64 splits and one wave per unit, and
+    # the whole-row K layouts of head_dim 64 and 256
+    (40000, 64, 64, 128), (20000, 32, None, 64), (12000, 128, 64, 64), (30000, 64, None, 256),
+    (12000, 32, 64, 256),
+])
+def test_paged_decode_equals_contiguous(total, block, splits, d):
+    hq, hkv = 24, 8
     cont, paged, bt, table, _, _ = make_pair(total, hq, hkv, d, block, 10 + total)
     cfg = R.AttnConfig.for_heads(hq, hkv, d)
     be = R.AdaptiveAttention(cfg, splits)
