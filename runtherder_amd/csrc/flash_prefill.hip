@@ -27,7 +27,8 @@
 //    the same scores as exact E4M3 codes times bf16 q.
 //  * Each lane owns one query row (the S^T column), so the softmax needs no
 //    cross-lane step except on a rebase. t = s * (k_scale * scale * log2 e)
-//    - m_ref against a lazy reference maximum; p = 2^t rounded to f16.
+//    - m_ref against a lazy reference maximum; p = 2^t rounded to f16, the
+//    row sum taken from the fp32 2^t.
 //  * V is dequantized into LDS as f16(code * v_scale), transposed to V^T in
 //    registers (v_perm) before the LDS write, and O^T += V^T P^T runs on
 //    v_mfma_f32_32x32x16_f16 with P^T straight from the score registers.
@@ -36,9 +37,10 @@
 //    of another as independent. One barrier per tile, which waits only for
 //    the K copy the next tile needs.
 //  * 8-wave workgroups run two phase-shifted groups so that the softmax
-//    (VALU) of one wave meets the MFMAs of the other wave on its SIMD; the
-//    4-wave workgroups weave the next tile's copies and V staging between
-//    their own MFMAs.
+//    (VALU) of one wave meets the MFMAs of the other wave on its SIMD, and a
+//    wave in its softmax or P V runs at a higher issue priority than one in
+//    its score MFMAs; the 4-wave workgroups weave the next tile's copies and
+//    V staging between their own MFMAs.
 #include "device_common.hpp"
 #include "launch.hpp"
 
