@@ -98,12 +98,57 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
 
 __device__ __forceinline__ int lane_id() { return static_cast<int>(threadIdx.x) & (kWave - 1); }
 
+// This lane's value and that of lane ^ mask, as a pair in some order. For
+// masks 16 and 32 a gfx950 row swap of v with itself (one VALU instruction:
+// v_permlane16_swap exchanges the odd 16-lane rows of its first operand with
+// the even rows of its second, v_permlane32_swap the upper 32 lanes of the
+// first with the lower 32 of the second) leaves every lane holding both;
+// other masks take a lane shuffle (an LDS crossbar round trip). Wave-wide
+// callers only: every lane of the wave must be active.
+struct LanePair {
+    float a, b;
+};
+__device__ __forceinline__ LanePair wave_xor_pair(float v, int mask) {
+    const uint32_t x = __float_as_uint(v);
+    if (mask == 32) {
+        const auto r = __builtin_amdgcn_permlane32_swap(x, x, false, false);
+        return {__uint_as_float(r[0]), __uint_as_float(r[1])};
+    }
+    if (mask == 16) {
+        const auto r = __builtin_amdgcn_permlane16_swap(x, x, false, false);
+        return {__uint_as_float(r[0]), __uint_as_float(r[1])};
+    }
+    return {v, __shfl_xor(v, mask, kWave)};
+}
+
+// The value of lane ^ mask. After v_permlane32_swap the first result holds
+// the lower 32 lanes' values and the second the upper's; after
+// v_permlane16_swap the first holds the even rows' and the second the odd
+// rows'.
+__device__ __forceinline__ float wave_xor_partner(float v, int mask) {
+    const uint32_t x = __float_as_uint(v);
+    const int      l = static_cast<int>(threadIdx.x) & (kWave - 1);
+    if (mask == 32) {
+        const auto r = __builtin_amdgcn_permlane32_swap(x, x, false, false);
+        return __uint_as_float((l & 32) ? r[0] : r[1]);
+    }
+    if (mask == 16) {
+        const auto r = __builtin_amdgcn_permlane16_swap(x, x, false, false);
+        return __uint_as_float((l & 16) ? r[0] : r[1]);
+    }
+    return __shfl_xor(v, mask, kWave);
+}
+
+// max / sum of this lane's value and lane ^ mask's (both lanes get the same
+// result, bit for bit).
 __device__ __forceinline__ float wave_xor_max(float v, int mask) {
-    return fmaxf(v, __shfl_xor(v, mask, kWave));
+    const LanePair p = wave_xor_pair(v, mask);
+    return fmaxf(p.a, p.b);
 }
 
 __device__ __forceinline__ float wave_xor_sum(float v, int mask) {
-    return v + __shfl_xor(v, mask, kWave);
+    const LanePair p = wave_xor_pair(v, mask);
+    return p.a + p.b;
 }
 
 }  // namespace rth

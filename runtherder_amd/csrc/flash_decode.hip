@@ -824,9 +824,9 @@ __global__ __launch_bounds__(kCombineThreads) void flash_decode_combine_kernel(
         f32x4 a2;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-            a2[e] = __shfl_xor(acc[e], mask);
+            a2[e] = wave_xor_partner(acc[e], mask);
         }
-        merge(__shfl_xor(m, mask), __shfl_xor(l, mask), a2);
+        merge(wave_xor_partner(m, mask), wave_xor_partner(l, mask), a2);
     }
     if (lane < kQuads) {
         sm_acc[wave][lane] = acc;
@@ -893,10 +893,10 @@ __device__ __forceinline__ float group_sum(float v) {
         v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x140, 0xF, 0xF, false));
     }
     if constexpr (N >= 32) {
-        v += __shfl_xor(v, 16, kWave);
+        v = wave_xor_sum(v, 16);
     }
     if constexpr (N >= 64) {
-        v += __shfl_xor(v, 32, kWave);
+        v = wave_xor_sum(v, 32);
     }
     return v;
 }
@@ -1077,14 +1077,14 @@ __global__ __launch_bounds__(kDecThreads) void flash_decode_valu_kernel(
     for (int mask = T::kLPK; mask < kWave; mask <<= 1) {
 #pragma unroll
         for (int h = 0; h < kVGroup; ++h) {
-            const float m2 = __shfl_xor(m_run[h], mask, kWave);
-            const float l2 = __shfl_xor(l_run[h], mask, kWave);
+            const float m2 = wave_xor_partner(m_run[h], mask);
+            const float l2 = wave_xor_partner(l_run[h], mask);
             const float M  = fmaxf(m_run[h], m2);
             const float f1 = (m_run[h] == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(m_run[h] - M);
             const float f2 = (m2 == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(m2 - M);
 #pragma unroll
             for (int e = 0; e < 16; ++e) {
-                const float a2 = __shfl_xor(acc[h][e], mask, kWave);
+                const float a2 = wave_xor_partner(acc[h][e], mask);
                 acc[h][e]      = acc[h][e] * f1 + a2 * f2;
             }
             l_run[h] = l_run[h] * f1 + l2 * f2;
