@@ -430,19 +430,19 @@ __global__ __launch_bounds__(kDecThreads) void flash_decode_kernel(
     const int  t_first   = (wj * n_tiles) / wn;
     const int  last_tile = ((wj + 1) * n_tiles) / wn - 1;
 
-    // Q^T as the B operand: column n = q head of the group (zero past G).
+    // Q^T as the B operand: column n = q head n of the group. Columns past
+    // G repeat head 0: their scores only ever mirror head 0's (so they never
+    // change the wave-wide lazy-max vote) and their m, l and O are never
+    // stored. Zeroing them instead made the wave wait for q before issuing
+    // its first K/V tile loads (measured 0.3-0.7 us per call at 8K).
     bf16x8 qop[T::kKSteps];
     {
-        const bool      has = n < G;
-        const uint16_t* qr  = q + static_cast<int64_t>(kvh * G + (has ? n : 0)) * D;
+        const uint16_t* qr = q + static_cast<int64_t>(kvh * G + (n < G ? n : 0)) * D;
 #pragma unroll
         for (int c = 0; c < T::kKChunks; ++c) {
 #pragma unroll
             for (int h = 0; h < 2; ++h) {
-                u32x4 w = *reinterpret_cast<const u32x4*>(qr + 16 * g + 64 * c + 8 * h);
-                if (!has) {
-                    w = u32x4{0u, 0u, 0u, 0u};
-                }
+                const u32x4 w = *reinterpret_cast<const u32x4*>(qr + 16 * g + 64 * c + 8 * h);
                 qop[2 * c + h] = __builtin_bit_cast(bf16x8, w);
             }
         }
