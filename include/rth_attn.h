@@ -81,8 +81,10 @@ int rth_default_num_splits(int num_kv_heads, int device);
  * attends *cache_len + 1 keys, split-K over num_splits key ranges with a
  * log-sum-exp merge (two kernels: splits, then merge). `partial` is
  * caller-owned scratch of rth_split_scratch_floats(Hq, D, num_splits) floats.
- * head_dim in {32,64,128,256,512}; 64/128/256 with Hq/Hkv <= 16 run the MFMA
- * split kernel, the rest the VALU split kernel (rth_decode_path). */
+ * head_dim in {32,64,128,256,512}; 64/128/256 run the MFMA split kernel when
+ * the group of G = Hq/Hkv q heads splits into equal blocks of 4..16 heads
+ * (G itself when G <= 16) with block * head_dim <= 2048, the rest the VALU
+ * split kernel (rth_decode_path). */
 int rth_attn_decode_split(uint16_t* out, const uint16_t* q, const uint8_t* k,
                           const uint8_t* v, const float* k_scale,
                           const float* v_scale, float* partial, int num_splits,

@@ -250,6 +250,24 @@ __host__ __device__ constexpr int dec_group_kv(int num_splits, int hkv, int cus)
     return 1;
 }
 
+// q blocks per cache kv head for the MFMA kernel (0: the shape goes to the
+// VALU kernel): the fewest blocks nqb dividing G with G / nqb <= 16 (the
+// MFMA's columns) and G / nqb * D within a wave's LDS staging row; blocks of
+// fewer than 4 q heads are left to the VALU kernel, whose units take 4.
+__host__ __device__ constexpr int dec_q_blocks(int hq, int hkv, int head_dim) {
+    if ((head_dim != 64 && head_dim != 128 && head_dim != 256) || hkv <= 0 || hq % hkv != 0) {
+        return 0;
+    }
+    const int G = hq / hkv;
+    for (int nqb = 1; nqb <= G; ++nqb) {
+        const int gb = G / nqb;
+        if (G % nqb == 0 && gb <= 16 && gb * head_dim <= kMaxGroupD) {
+            return (gb >= 4 || nqb == 1) ? nqb : 0;
+        }
+    }
+    return 0;
+}
+
 __host__ __device__ constexpr int dec_workgroups(int num_splits, int hkv, int kvg) {
     return (kvg > 0) ? num_splits * (hkv / kvg)
                      : (num_splits * hkv + kDecWaves - 1) / kDecWaves;
@@ -262,7 +280,8 @@ template <int D>
 __device__ __forceinline__ void quantize_new_token(TileRaw<D>& vt, const uint16_t* __restrict__ kx,
                                                    const uint16_t* __restrict__ vx,
                                                    uint8_t* kc_row, uint8_t* vc_row,
-                                                   float* ks_slot, float* vs_slot, int lane) {
+                                                   float* ks_slot, float* vs_slot, int lane,
+                                                   bool write) {
     using T     = DecTraits<D>;
     const int n = lane & 15;
     const int g = lane >> 4;
@@ -335,7 +354,9 @@ __device__ __forceinline__ void quantize_new_token(TileRaw<D>& vt, const uint16_
         cw.w = code4(kw[c][1].z, kw[c][1].w, kinv);
         if (n == 0) {
             vt.kraw[0][c] = cw;
-            *reinterpret_cast<u32x4*>(kc_row + 16 * g + 64 * c) = cw;
+            if (write) {
+                *reinterpret_cast<u32x4*>(kc_row + 16 * g + 64 * c) = cw;
+            }
         }
     }
 #pragma unroll
@@ -343,11 +364,13 @@ __device__ __forceinline__ void quantize_new_token(TileRaw<D>& vt, const uint16_
         const uint32_t cw = code4(vw[2 * w], vw[2 * w + 1], vinv);
         if (g == 0) {
             vt.vraw[0][w] = cw;
-            *reinterpret_cast<uint32_t*>(vc_row + T::kVBytes * n + 4 * w) = cw;
+            if (write) {
+                *reinterpret_cast<uint32_t*>(vc_row + T::kVBytes * n + 4 * w) = cw;
+            }
         }
     }
     vt.sc = (lane == 0) ? ksc : ((lane == 32) ? vsc : 0.0f);
-    if (lane == 0) {
+    if (write && lane == 0) {
         *ks_slot = ksc;
         *vs_slot = vsc;
     }
@@ -358,6 +381,12 @@ __device__ __forceinline__ void quantize_new_token(TileRaw<D>& vt, const uint16_
 // it, stores codes and scales, and attends to it from registers, so no wave
 // reads the row being written.
 // kPaged: K/V/scale rows are addressed through block_table (see paged_row).
+// nqb: q blocks per cache kv head. A group of more than 16 q heads (the
+// MFMA's 16 columns) is served as nqb virtual kv heads of G / nqb q heads
+// each: `hkv` counts virtual heads (cache heads x nqb), virtual head kvh reads
+// the K/V rows of cache head kvh / nqb, and q heads, partial slots and the
+// merge keep their global q-head index (kvh * G + n). Only the first virtual
+// head of a cache head stores the appended token.
 template <int D, bool kAppend, bool kPaged>
 __global__ __launch_bounds__(kDecThreads) void flash_decode_kernel(
     const uint16_t* __restrict__ q, const uint8_t* __restrict__ k,
@@ -366,7 +395,7 @@ __global__ __launch_bounds__(kDecThreads) void flash_decode_kernel(
     const int* __restrict__ cache_len, int hq, int hkv, float scale_log2,
     const uint16_t* __restrict__ k_new, const uint16_t* __restrict__ v_new,
     uint8_t* k_w, uint8_t* v_w, float* ks_w, float* vs_w,
-    const int* __restrict__ block_table, int block_shift, int kvg) {
+    const int* __restrict__ block_table, int block_shift, int kvg, int nqb) {
     using T = DecTraits<D>;
 
     __shared__ __attribute__((aligned(16))) float sm_sc[kDecWaves][64];
@@ -413,6 +442,8 @@ __global__ __launch_bounds__(kDecThreads) void flash_decode_kernel(
     if (si >= pt.n_eff) {   // uniform per workgroup in coop mode
         return;
     }
+    const int kvc = kvh / nqb;   // cache kv head
+    const int hkc = hkv / nqb;   // cache kv heads
     const int k0 = split_tile(pt, si) * kTileKeys;
     // With an append, the split holding the new key (the last one) reads
     // only the keys before it from the cache; one of its waves adds the new
@@ -575,7 +606,7 @@ __global__ __launch_bounds__(kDecThreads) void flash_decode_kernel(
         uint8_t* kbuf = reinterpret_cast<uint8_t*>(sm_o[wave]);
         auto stream = [&]<bool kNT>() {
             auto load = [&](TileRaw<D>& t, int kb) {
-                load_tile<D, kNT>(t, k, v, ks, vs, kb, k1, kvh, hkv, lane, tile_delta(kb));
+                load_tile<D, kNT>(t, k, v, ks, vs, kb, k1, kvc, hkc, lane, tile_delta(kb));
             };
             TileRaw<D> ring[kRing];
 #pragma unroll
@@ -619,10 +650,10 @@ __global__ __launch_bounds__(kDecThreads) void flash_decode_kernel(
     if (kAppend && virt) {
         TileRaw<D>    vt;
         const int     prow = kPaged ? paged_row(p_new, block_table, block_shift) : p_new;
-        const int64_t row  = static_cast<int64_t>(prow) * hkv + kvh;
-        quantize_new_token<D>(vt, k_new + static_cast<int64_t>(kvh) * D,
-                              v_new + static_cast<int64_t>(kvh) * D, k_w + row * D,
-                              v_w + row * D, ks_w + row, vs_w + row, lane);
+        const int64_t row  = static_cast<int64_t>(prow) * hkc + kvc;
+        quantize_new_token<D>(vt, k_new + static_cast<int64_t>(kvc) * D,
+                              v_new + static_cast<int64_t>(kvc) * D, k_w + row * D,
+                              v_w + row * D, ks_w + row, vs_w + row, lane, kvh == kvc * nqb);
         process(vt, p_new, p_new + 1);
     }
 
@@ -852,11 +883,12 @@ __global__ __launch_bounds__(kCombineThreads) void flash_decode_combine_kernel(
 
 // ---- VALU split kernel -------------------------------------------------------
 // Serves the shapes the MFMA kernel does not (head_dim 32 and 512, GQA groups
-// above 16) with the same partition (one wave per (kv head, split, block of
-// kVGroup q heads) unit at every context; kvg = -1 for the merge), the same
-// scratch and the same merge kernel. No MFMA: a key row of D E4M3 bytes is
-// spread over D / 16 lanes, 16 bytes per lane (one coalesced 128-bit load of
-// K and one of V), so a wave takes 64 / (D / 16) keys per step. Each lane
+// that do not split into blocks of 4-16 q heads) with the same partition (one
+// wave per (kv head, split, block of kVGroup q heads) unit at every context;
+// kvg = -1 for the merge), the same scratch and the same merge kernel. No
+// MFMA: a key row of D E4M3 bytes is spread over D / 16 lanes, 16 bytes per
+// lane (one coalesced 128-bit load of K and one of V), so a wave takes
+// 64 / (D / 16) keys per step. Each lane
 // converts its 16 codes exactly to bf16 (K) and fp32 (V) in registers, takes
 // its share of q . k with v_dot2c_f32_bf16, and the partial dots of a key
 // are summed by DPP row exchanges (quad_perm, row_half_mirror, row_mirror:
@@ -1156,19 +1188,24 @@ hipError_t launch_decode(uint16_t* out, const uint16_t* q, const uint8_t* k,
     if (ce != hipSuccess) {
         return ce;
     }
-    const int  kvg   = dec_group_kv(num_splits, hkv, cus);
-    const int  n_wgs = dec_workgroups(num_splits, hkv, kvg);
+    const int nqb = dec_q_blocks(hq, hkv, D);
+    if (nqb == 0) {
+        return hipErrorInvalidValue;
+    }
+    const int  hkv_v = hkv * nqb;   // virtual kv heads of at most 16 q heads each
+    const int  kvg   = dec_group_kv(num_splits, hkv_v, cus);
+    const int  n_wgs = dec_workgroups(num_splits, hkv_v, kvg);
     const dim3 grid(static_cast<unsigned>(n_wgs));
     if (k_new != nullptr) {
         hipLaunchKernelGGL((flash_decode_kernel<D, true, kPaged>), grid, dim3(kDecThreads), 0,
-                           stream, q, k, v, ks, vs, partial, num_splits, cache_len, hq, hkv,
+                           stream, q, k, v, ks, vs, partial, num_splits, cache_len, hq, hkv_v,
                            scale * kLog2e, k_new, v_new, k_w, v_w, ks_w, vs_w, block_table,
-                           block_shift, kvg);
+                           block_shift, kvg, nqb);
     } else {
         hipLaunchKernelGGL((flash_decode_kernel<D, false, kPaged>), grid, dim3(kDecThreads), 0,
-                           stream, q, k, v, ks, vs, partial, num_splits, cache_len, hq, hkv,
+                           stream, q, k, v, ks, vs, partial, num_splits, cache_len, hq, hkv_v,
                            scale * kLog2e, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr,
-                           block_table, block_shift, kvg);
+                           block_table, block_shift, kvg, nqb);
     }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) {
@@ -1223,9 +1260,7 @@ std::size_t decode_scratch_floats(int num_q_heads, int head_dim, int max_splits)
 }
 
 bool decode_mfma_supported(int num_q_heads, int num_kv_heads, int head_dim) {
-    const int G = num_q_heads / num_kv_heads;
-    return (head_dim == 64 || head_dim == 128 || head_dim == 256) && G <= 16 &&
-           G * head_dim <= kMaxGroupD;
+    return dec_q_blocks(num_q_heads, num_kv_heads, head_dim) > 0;
 }
 
 hipError_t flash_decode_launch(uint16_t* out, const uint16_t* q,

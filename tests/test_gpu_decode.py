@@ -176,15 +176,15 @@ def test_grouped_workgroups(ctx, hq, hkv, splits, d):
 
 @pytest.mark.parametrize("cache_len,hq,hkv,d,splits", [
     (8191, 8, 2, 32, None), (131071, 32, 8, 32, 64), (9000, 16, 4, 512, 64),
-    (65535, 8, 2, 512, None), (10000, 64, 2, 128, None), (5000, 40, 2, 64, 100),
+    (65535, 8, 2, 512, None), (10000, 36, 4, 256, None), (5000, 34, 2, 64, 100),
     (40, 32, 8, 32, 4), (3, 8, 2, 512, 8), (2999, 68, 4, 256, 32),
 ])
 def test_valu_split_kernel(cache_len, hq, hkv, d, splits):
     """Shapes the MFMA split kernel does not take (head_dim 32 and 512, GQA
-    groups above 16) run the VALU split kernel (reference
-    src/kernels/flash_decode.cu:296-319 serves all five head sizes with one
-    split kernel): contexts up to 128K, ragged head blocks (20 and 17 q heads
-    per kv head), more splits than tiles."""
+    groups that do not split into blocks of 4-16 q heads) run the VALU split
+    kernel (reference src/kernels/flash_decode.cu:296-319 serves all five head
+    sizes with one split kernel): contexts up to 128K, ragged head blocks (17
+    and 9 q heads per kv head), more splits than tiles."""
     assert R.decode_path(hq, hkv, d) == R.DECODE_VALU
     scale = np.float32(1.0 / np.sqrt(d))
     splits = splits or R.default_num_splits(hkv)
@@ -194,12 +194,35 @@ def test_valu_split_kernel(cache_len, hq, hkv, d, splits):
     check(got, q, k8, v8, ks, vs, cache_len, hq, hkv, d, scale)
 
 
+@pytest.mark.parametrize("cache_len,hq,hkv,d,splits", [
+    (10000, 64, 2, 128, None), (5000, 40, 2, 64, 100), (8195, 32, 1, 128, None),
+    (3000, 96, 2, 128, 64), (4000, 16, 1, 256, 32), (20000, 24, 1, 128, None),
+    (30000, 64, 2, 128, 16), (2040, 48, 2, 256, 8), (100, 128, 4, 64, 3),
+])
+def test_mfma_q_blocks(cache_len, hq, hkv, d, splits):
+    """GQA groups wider than the MFMA's 16 columns (or than a wave's 2048-value
+    staging row) run the MFMA kernel as blocks of 4-16 q heads per kv head
+    (two blocks of 16, of 10, of 12, three of 16, two of 8 at head_dim 256),
+    one-kv-head (MQA) caches, grouped workgroups at 16 splits; oracle parity."""
+    assert R.decode_path(hq, hkv, d) == R.DECODE_MFMA
+    scale = np.float32(1.0 / np.sqrt(d))
+    splits = splits or R.default_num_splits(hkv)
+    q = O.normal_bf16((hq, d), 71 + hq)
+    _, _, k8, v8, ks, vs = make_cache(cache_len + 1, hkv, d, kind="normal", seed=cache_len + hq)
+    got = gpu_decode(q, k8, v8, ks, vs, cache_len, hq, hkv, d, splits, scale)
+    check(got, q, k8, v8, ks, vs, cache_len, hq, hkv, d, scale)
+
+
 def test_decode_path_selection():
     """The reference test shapes with head_dim 32 / 512 take the VALU kernel;
     head_dim 64 / 128 / 256 with groups up to 16 the MFMA kernel."""
     assert R.decode_path(32, 8, 32) == R.DECODE_VALU
     assert R.decode_path(8, 2, 512) == R.DECODE_VALU
-    assert R.decode_path(64, 2, 128) == R.DECODE_VALU
+    assert R.decode_path(68, 4, 256) == R.DECODE_VALU    # 17 q heads: no blocks of 4-16
+    assert R.decode_path(36, 4, 256) == R.DECODE_VALU    # 9 x 256 > 2048, blocks of 3
+    assert R.decode_path(64, 2, 128) == R.DECODE_MFMA    # two blocks of 16
+    assert R.decode_path(16, 1, 256) == R.DECODE_MFMA    # two blocks of 8
+    assert R.decode_path(96, 2, 64) == R.DECODE_MFMA     # three blocks of 16
     for d in (64, 128, 256):
         assert R.decode_path(32, 8, d) == R.DECODE_MFMA
     assert R.decode_path(64, 4, 128) == R.DECODE_MFMA
@@ -248,6 +271,8 @@ def test_score_dynamic_range(splits):
     (2040, 24, 8, 128, None), (8195, 24, 8, 128, None), (9000, 32, 8, 128, 64),
     (130, 8, 2, 64, 8), (700, 8, 4, 256, 16), (77, 64, 4, 128, 4), (40, 8, 2, 32, 4),
     (5000, 32, 8, 128, 128), (6000, 16, 4, 128, 128),
+    # q blocks: several units per cache head attend the new token, one stores it
+    (700, 64, 2, 128, 16), (3000, 32, 1, 128, None), (130, 16, 1, 256, 8),
 ])
 def test_decode_append_fused(cache_len, hq, hkv, d, splits):
     """Fused append + decode: the cache row equals the append kernel's bytes

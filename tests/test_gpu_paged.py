@@ -92,7 +92,19 @@ def test_paged_append_bytes(total, block):
     (12000, 32, 64, 256),
 ])
 def test_paged_decode_equals_contiguous(total, block, splits, d):
-    hq, hkv = 24, 8
+    paged_decode_case(total, block, splits, d, 24, 8)
+
+
+@pytest.mark.parametrize("total,block,splits,d,hq,hkv", [
+    (5000, 64, None, 128, 64, 2), (3001, 32, 16, 256, 16, 1), (900, 128, 7, 64, 96, 2),
+])
+def test_paged_decode_q_blocks(total, block, splits, d, hq, hkv):
+    """Groups wider than 16 q heads (blocks of q heads reading one cache head)
+    through the block table."""
+    paged_decode_case(total, block, splits, d, hq, hkv)
+
+
+def paged_decode_case(total, block, splits, d, hq, hkv):
     cont, paged, bt, table, _, _ = make_pair(total, hq, hkv, d, block, 10 + total)
     cfg = R.AttnConfig.for_heads(hq, hkv, d)
     be = R.AdaptiveAttention(cfg, splits)
@@ -110,9 +122,10 @@ def test_paged_decode_equals_contiguous(total, block, splits, d):
     assert np.array_equal(bf16_host(o1), got)
 
 
-@pytest.mark.parametrize("total,block", [(2041, 64), (9000, 32)])
-def test_paged_fused_append_decode_equals_contiguous(total, block):
-    hq, hkv, d = 24, 8, 128
+@pytest.mark.parametrize("total,block,hq,hkv", [(2041, 64, 24, 8), (9000, 32, 24, 8),
+                                                (3000, 64, 64, 2)])
+def test_paged_fused_append_decode_equals_contiguous(total, block, hq, hkv):
+    d = 128
     cont, paged, bt, table, k, v = make_pair(total - 1, hq, hkv, d, block, 30 + total)
     cfg = R.AttnConfig.for_heads(hq, hkv, d)
     be = R.AdaptiveAttention(cfg)
