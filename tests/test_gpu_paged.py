@@ -153,9 +153,10 @@ def test_paged_fused_append_decode_equals_contiguous(total, block, hq, hkv):
 
 # Workgroup shapes on 256 compute units: 1021 and 3000 @ 2237 take the
 # key-split kernel, 200 (two 128-row blocks per head, whole grid resident) the
-# 4-wave kernel with heavy/light pairing, 4096 the 8-wave kernel.
+# 4-wave kernel with heavy/light pairing, 2500 the 4-wave kernel over two
+# rounds (early-issue prologue), 4096 the 8-wave kernel.
 @pytest.mark.parametrize("total,clen,block", [(1021, 0, 64), (3000, 2237, 32), (4096, 0, 128),
-                                              (200, 0, 32), (1300, 1100, 64)])
+                                              (200, 0, 32), (1300, 1100, 64), (2500, 0, 64)])
 def test_paged_prefill_equals_contiguous(total, clen, block):
     hq, hkv, d = 32, 8, 128
     cont, paged, bt, table, _, _ = make_pair(total, hq, hkv, d, block, 50 + total)
