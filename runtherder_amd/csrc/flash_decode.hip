@@ -9,7 +9,8 @@
 //    is read from HBM once, not Hq/Hkv times.
 //  * Scores and the value product run on bf16 MFMA (v_mfma_f32_16x16x32_bf16)
 //    with the GQA group as the 16-wide N dimension: S^T = K Q^T, then
-//    O^T += V^T P^T. E4M3 codes convert exactly to bf16 in registers
+//    O^T += V^T P^T. Groups wider than 16 q heads run as equal blocks of
+//    4-16 q heads, each block a unit of its own over the same K/V rows. E4M3 codes convert exactly to bf16 in registers
 //    (v_cvt_scalef32_pk_bf16_fp8); the per-(token, kv_head) scales are folded
 //    in fp32 into the score column (k_scale) and into P (v_scale).
 //  * K is loaded as whole rows (16 bytes per lane) and moved into the MFMA
