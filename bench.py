@@ -164,6 +164,46 @@ def bench_decode(torch, R, args, stream):
     value_gbs = total_bytes / (timed[True] * 1e-3) / 1e9
     unfused_gbs = total_bytes / (timed[False] * 1e-3) / 1e9
 
+    # The same steps with RoPE in them (the engine's per-layer sequence
+    # rope -> append -> run): the fused RoPE entry (2 launches per layer),
+    # rope_bf16 + the fused append/decode (3), and the reference's order
+    # rope_bf16 + append + run (4). One 128-step graph each, replayed twice
+    # after one warmup replay; rope_bf16 rotates the stored q/k in place.
+    inv = (5e5 ** (-torch.arange(0, d, 2, dtype=torch.float64, device=dev) / d)).float()
+    torch.cuda.synchronize()
+
+    def run_rope_steps(mode, n_steps):
+        for s in range(n_steps):
+            for l in range(L):
+                q, k, v, o, view = qs[s, l], ks[s, l], vs[s, l], out[s, l], cache.view(l)
+                if mode == "fused":
+                    backend.run_decode_rope_append(o, q, view, k, v, pos, inv, pos)
+                elif mode == "rope+fused":
+                    R.rope_bf16(q, k, pos, inv, 1, hq, hkv, d)
+                    backend.run_decode_append(o, q, view, k, v, pos)
+                else:
+                    R.rope_bf16(q, k, pos, inv, 1, hq, hkv, d)
+                    cache.append(l, k, v, 1, pos)
+                    backend.run(o, q, view, 1, pos)
+            R.advance_position(pos, 1)
+        R.advance_position(pos, -n_steps)
+
+    rope_ms = {}
+    for mode in ("fused", "rope+fused", "reference"):
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=stream):
+            run_rope_steps(mode, GRAPH_STEPS)
+        torch.cuda.synchronize()
+        with torch.cuda.stream(stream):
+            g.replay()
+            torch.cuda.synchronize()
+            with EventTimer(torch, stream) as t:
+                g.replay()
+                g.replay()
+        torch.cuda.synchronize()
+        rope_ms[mode] = t.ms / (2 * GRAPH_STEPS)
+        del g
+
     # Dominant kernels alone: one decode call (split kernel + merge kernel) per
     # layer, rotating over the 28 layers (defeats the 256 MB Infinity Cache),
     # captured back to back in a graph and timed with HIP events on its stream.
@@ -187,6 +227,7 @@ def bench_decode(torch, R, args, stream):
     return {
         "value": value_gbs, "ms_per_step": ms_per_step, "steps": steps,
         "unfused_value": unfused_gbs, "unfused_ms_per_step": timed[False] / steps,
+        "rope_ms_per_step": rope_ms, "rope_step_bytes": sum(step_bytes) / GRAPH_STEPS,
         "warmup": max(0, args.warmup), "ctx": ctx0, "splits": backend.num_splits,
         "kernel_us": kern_us, "kernel_bytes": kbytes, "kernel_gbs": achieved,
         "cache": cache, "qs": qs, "depth": depth, "hq": hq, "hkv": hkv, "d": d,
@@ -598,6 +639,18 @@ def main() -> int:
             "ms_per_step": round(dec["unfused_ms_per_step"], 4),
             "workload": "the same steps as KVCache.append then AdaptiveAttention.run (3 kernels "
                         "per layer, the reference's call sequence)",
+        },
+        "decode_step_rope": {
+            "unit": "ms/step (28 layers)",
+            "fused": round(dec["rope_ms_per_step"]["fused"], 4),
+            "rope_then_fused_append_decode": round(dec["rope_ms_per_step"]["rope+fused"], 4),
+            "reference_order": round(dec["rope_ms_per_step"]["reference"], 4),
+            "fused_gbs": round(dec["rope_step_bytes"] / (dec["rope_ms_per_step"]["fused"] * 1e-3)
+                               / 1e9, 1),
+            "workload": "the decode steps with RoPE (theta 5e5) of q and the new k: "
+                        "rth_attn_decode_rope_append_split (2 kernels per layer) vs rope_bf16 + "
+                        "the fused append/decode (3) vs rope_bf16 + append + run (4, the "
+                        "reference's order); 128-step graphs",
         },
         "cpu_baseline": cpu,
     }

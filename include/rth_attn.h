@@ -216,6 +216,34 @@ int rth_attn_decode_append_split_paged(uint16_t* out, const uint16_t* q, uint8_t
                                        float* partial, int num_splits, const int* cache_len,
                                        int num_q_heads, int num_kv_heads, int head_dim,
                                        float scale, void* stream);
+/* No counterpart in the reference: fuses the per-layer decode step
+ * rope_bf16(q, k, positions, inv_freq) -> KVCache::append(layer, k, v, 1,
+ * cache_len) -> AttentionBackend::run(out, q, view, 1, cache_len) (reference
+ * src/model/supported/llama/llama3.cu:228-234) into the two launches of
+ * rth_attn_decode_append_split. q and k_new ([Hq, D] and [Hkv, D] bf16,
+ * unrotated) are read only: both are rotated in registers by the angles of
+ * positions[0] with rth_rope_bf16's arithmetic, so the cache row written at
+ * *cache_len is byte-identical to rth_rope_bf16 + rth_kv_append_fp8 and the
+ * output equals rth_attn_decode_append_split on the rotated q and k. Shapes
+ * rth_decode_path reports as RTH_DECODE_MFMA (head_dim 64, 128, 256); others
+ * fail with an error. block_table == NULL (or the first entry point): the
+ * contiguous layout. */
+int rth_attn_decode_rope_append_split(uint16_t* out, const uint16_t* q, uint8_t* k_cache,
+                                      uint8_t* v_cache, float* k_scale, float* v_scale,
+                                      const uint16_t* k_new, const uint16_t* v_new,
+                                      const int* positions, const float* inv_freq,
+                                      float* partial, int num_splits, const int* cache_len,
+                                      int num_q_heads, int num_kv_heads, int head_dim,
+                                      float scale, void* stream);
+int rth_attn_decode_rope_append_split_paged(uint16_t* out, const uint16_t* q, uint8_t* k_cache,
+                                            uint8_t* v_cache, float* k_scale, float* v_scale,
+                                            const int* block_table, int block_size,
+                                            const uint16_t* k_new, const uint16_t* v_new,
+                                            const int* positions, const float* inv_freq,
+                                            float* partial, int num_splits,
+                                            const int* cache_len, int num_q_heads,
+                                            int num_kv_heads, int head_dim, float scale,
+                                            void* stream);
 int rth_attn_prefill_paged(uint16_t* out, const uint16_t* q, const uint8_t* k,
                            const uint8_t* v, const float* k_scale, const float* v_scale,
                            const int* block_table, int block_size, int n_new,

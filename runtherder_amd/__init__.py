@@ -24,6 +24,7 @@ from .ops import (  # noqa: F401
     set_decode_kernel,
     default_num_splits,
     flash_decode_append_split_bf16,
+    flash_decode_rope_append_split_bf16,
     flash_decode_split_bf16,
     flash_decode_split_bf16_noalloc,
     flash_prefill_bf16,

@@ -51,6 +51,11 @@ _SIGNATURES = {
     "rth_attn_decode_append_split_paged": (_c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_int,
                                                     _vp, _vp, _vp, _c_int, _vp, _c_int, _c_int,
                                                     _c_int, ctypes.c_float, _vp]),
+    "rth_attn_decode_rope_append_split": (_c_int, [_vp] * 11 + [_c_int, _vp, _c_int, _c_int,
+                                                                _c_int, ctypes.c_float, _vp]),
+    "rth_attn_decode_rope_append_split_paged": (_c_int, [_vp] * 7 + [_c_int] + [_vp] * 5 +
+                                                [_c_int, _vp, _c_int, _c_int, _c_int,
+                                                 ctypes.c_float, _vp]),
     "rth_attn_prefill_paged": (_c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_int, _c_int, _vp,
                                         _c_int, _c_int, _c_int, ctypes.c_float, _vp]),
 }

@@ -52,6 +52,7 @@ constexpr int kDecWaves   = 8;
 constexpr int kDecThreads = kDecWaves * kWave;
 constexpr int kTileKeys   = 32;     // keys per wave iteration (two 16-key MFMAs)
 constexpr int kMaxGroupD  = 2048;   // G * head_dim bound of a wave's LDS partial staging
+constexpr int kMaxD       = 256;    // largest head_dim of the MFMA decode kernel
 constexpr int kCombineThreads = 128;
 constexpr int kCombineSlice   = 16;    // head_dim slice per merge workgroup
 constexpr int kNtMinTiles     = 2;     // tiles past the first a wave streams with nontemporal loads
@@ -274,15 +275,97 @@ __host__ __device__ constexpr int dec_workgroups(int num_splits, int hkv, int kv
                      : (num_splits * hkv + kDecWaves - 1) / kDecWaves;
 }
 
+// Rotate-half RoPE of the bf16 words a lane holds of one head row (the q
+// load and new-token layout: chunk c, half h, word i = elements
+// 16g + 64c + 8h + 2i, +1), as rope_bf16 computes it (rope.hip): element d
+// pairs with d + D/2 by angle theta_f, f = d mod D/2, with
+// a' = bf16(fma(a, cos, -(b sin))), b' = bf16(fma(a, sin, b cos)); rc/rs hold
+// cos/sin of the D/2 angles. The partner words sit in the same lane (chunk
+// c ^ (kKChunks/2)) for D 128 and 256, in lane l ^ 32 for D 64.
+template <int D>
+__device__ __forceinline__ void rope_row_words(u32x4 (&w)[DecTraits<D>::kKChunks][2],
+                                               const float* rc, const float* rs, int lane) {
+    using T     = DecTraits<D>;
+    const int g = lane >> 4;
+    // Rotates word i of a and b (8 angles from f0) as pairs of bf16.
+    auto rot = [&](uint32_t a, uint32_t b, int f, uint32_t& ra, uint32_t& rb) {
+        float oa[2], ob[2];
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+            const float x  = __uint_as_float(e ? (a & 0xffff0000u) : (a << 16));
+            const float y  = __uint_as_float(e ? (b & 0xffff0000u) : (b << 16));
+            const float co = rc[f + e];
+            const float si = rs[f + e];
+            oa[e]          = fmaf(x, co, -(y * si));
+            ob[e]          = fmaf(x, si, y * co);
+        }
+        ra = pack_bf16x2(oa[0], oa[1]);
+        rb = pack_bf16x2(ob[0], ob[1]);
+    };
+    if constexpr (D == 64) {
+        // Lanes 0-31 hold elements 0-31 (a), lanes 32-63 their partners (b).
+        const bool first = g < 2;
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const uint32_t own  = w[0][h][i];
+                const uint32_t part = __float_as_uint(wave_xor_partner(__uint_as_float(own), 32));
+                uint32_t       ra, rb;
+                rot(first ? own : part, first ? part : own, 16 * (g & 1) + 8 * h + 2 * i, ra, rb);
+                w[0][h][i] = first ? ra : rb;
+            }
+        }
+    } else {
+        constexpr int kHalf = T::kKChunks / 2;
+#pragma unroll
+        for (int c = 0; c < kHalf; ++c) {
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    uint32_t ra, rb;
+                    rot(w[c][h][i], w[c + kHalf][h][i], 16 * g + 64 * c + 8 * h + 2 * i, ra, rb);
+                    w[c][h][i]         = ra;
+                    w[c + kHalf][h][i] = rb;
+                }
+            }
+        }
+    }
+}
+
+// cos / sin of the D/2 RoPE angles float(pos) * inv_freq[f] into rc / rs,
+// taken in double precision and rounded to fp32 as rope_bf16 does; one wave.
+// inv[j] = inv_freq[lane + 64 j], loaded ahead (see decode_body).
+constexpr int kRopeIter = kMaxD / 2 / kWave;   // angles per lane at the largest head_dim
+template <int D>
+__device__ __forceinline__ void rope_table_wave(float* rc, float* rs, int pos,
+                                                const float (&inv)[kRopeIter], int lane) {
+#pragma unroll 1
+    for (int j = 0; j * kWave < D / 2; ++j) {   // one double sincos live at a time
+        const int f = lane + j * kWave;
+        if (f >= D / 2) {
+            break;
+        }
+        const float th = static_cast<float>(pos) * inv[j];
+        double      sn, cs;
+        sincos(static_cast<double>(th), &sn, &cs);
+        rc[f] = static_cast<float>(cs);
+        rs[f] = static_cast<float>(sn);
+    }
+    __builtin_amdgcn_wave_barrier();
+}
+
 // The appended token's quantized K/V codes for one (kv head) unit, laid out
 // as the tile registers of key 0 of a tile after k_rows_to_mfma, plus the
-// scales.
+// scales. rc != nullptr: K is rotated first (RoPE, see rope_row_words).
 template <int D>
 __device__ __forceinline__ void quantize_new_token(TileRaw<D>& vt, const uint16_t* __restrict__ kx,
                                                    const uint16_t* __restrict__ vx,
                                                    uint8_t* kc_row, uint8_t* vc_row,
                                                    float* ks_slot, float* vs_slot, int lane,
-                                                   bool write) {
+                                                   bool write, const float* rc = nullptr,
+                                                   const float* rs = nullptr) {
     using T     = DecTraits<D>;
     const int n = lane & 15;
     const int g = lane >> 4;
@@ -295,6 +378,15 @@ __device__ __forceinline__ void quantize_new_token(TileRaw<D>& vt, const uint16_
         for (int h = 0; h < 2; ++h) {
             kw[c][h] = (n == 0) ? *reinterpret_cast<const u32x4*>(kx + 16 * g + 64 * c + 8 * h)
                                 : u32x4{0u, 0u, 0u, 0u};
+        }
+    }
+    if (rc != nullptr) {
+        rope_row_words<D>(kw, rc, rs, lane);
+    }
+#pragma unroll
+    for (int c = 0; c < T::kKChunks; ++c) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 kmax = fmaxf(kmax, fabsf(__uint_as_float(kw[c][h][e] << 16)));
@@ -388,21 +480,29 @@ __device__ __forceinline__ void quantize_new_token(TileRaw<D>& vt, const uint16_
 // the K/V rows of cache head kvh / nqb, and q heads, partial slots and the
 // merge keep their global q-head index (kvh * G + n). Only the first virtual
 // head of a cache head stores the appended token.
-template <int D, bool kAppend, bool kPaged>
-__global__ __launch_bounds__(kDecThreads) void flash_decode_kernel(
+// kRope (with kAppend): q and the appended k row are rotated in registers by
+// the angles of positions[0] (rope_bf16's arithmetic, see rope_row_words);
+// each wave builds its own cos/sin table after issuing its first tile loads.
+template <int D, bool kAppend, bool kPaged, bool kRope>
+__device__ __forceinline__ void decode_body(
     const uint16_t* __restrict__ q, const uint8_t* __restrict__ k,
     const uint8_t* __restrict__ v, const float* __restrict__ ks,
     const float* __restrict__ vs, float* __restrict__ partial, int num_splits,
     const int* __restrict__ cache_len, int hq, int hkv, float scale_log2,
     const uint16_t* __restrict__ k_new, const uint16_t* __restrict__ v_new,
     uint8_t* k_w, uint8_t* v_w, float* ks_w, float* vs_w,
-    const int* __restrict__ block_table, int block_shift, int kvg, int nqb) {
+    const int* __restrict__ block_table, int block_shift, int kvg, int nqb,
+    const int* __restrict__ positions, const float* __restrict__ inv_freq) {
     using T = DecTraits<D>;
+    static_assert(!kRope || kAppend, "the RoPE variant is the fused decode step");
 
     __shared__ __attribute__((aligned(16))) float sm_sc[kDecWaves][64];
     __shared__ __attribute__((aligned(16))) float sm_o[kDecWaves][kMaxGroupD];
     __shared__ float sm_m[kDecWaves][16];
     __shared__ float sm_l[kDecWaves][16];
+    // kRope: cos (first D/2) and sin (next D/2) of the RoPE angles, built by
+    // wave 0 for the whole workgroup.
+    __shared__ __attribute__((aligned(16))) float sm_rope[kMaxD];
 
     const int G    = hq / hkv;
     const int tid  = static_cast<int>(threadIdx.x);
@@ -440,7 +540,31 @@ __global__ __launch_bounds__(kDecThreads) void flash_decode_kernel(
         }
         kvh = grp * pt.gkv + wave % pt.gkv;
     }
+    // kRope: the angle inputs are loaded here, ahead of every tile load, so
+    // building the table later waits for nothing else in flight; every wave
+    // passes exactly one workgroup barrier, the one after which wave 0's
+    // table is complete (a wave without keys passes it here).
+    [[maybe_unused]] float rope_inv[kRopeIter] = {};
+    [[maybe_unused]] int   rope_pos            = 0;
+    if constexpr (kRope) {
+        rope_pos = *positions;
+#pragma unroll
+        for (int j = 0; j < kRopeIter; ++j) {
+            if (lane + j * kWave < D / 2) {
+                rope_inv[j] = inv_freq[lane + j * kWave];
+            }
+        }
+    }
+    auto rope_sync = [&]() {
+        if constexpr (kRope) {
+            if (wave == 0) {
+                rope_table_wave<D>(sm_rope, sm_rope + D / 2, rope_pos, rope_inv, lane);
+            }
+            __syncthreads();
+        }
+    };
     if (si >= pt.n_eff) {   // uniform per workgroup in coop mode
+        rope_sync();
         return;
     }
     const int kvc = kvh / nqb;   // cache kv head
@@ -487,6 +611,38 @@ __global__ __launch_bounds__(kDecThreads) void flash_decode_kernel(
     }
     float m_run = -INFINITY;
     float l_run = 0.0f;
+
+    // kRope: the table barrier, then q rotated in registers. The barrier
+    // goes behind the first tile loads, except at head_dim 256 (a one-tile
+    // ring), where the table is built before any tile registers are live
+    // (behind them its double-precision sincos spilled).
+    constexpr bool kTableFirst = kRope && D == 256;
+    if constexpr (kTableFirst) {
+        rope_sync();
+    }
+    auto rope_q = [&]() {
+        if constexpr (kRope) {
+            if constexpr (!kTableFirst) {
+                rope_sync();
+            }
+            u32x4 qw[T::kKChunks][2];
+#pragma unroll
+            for (int c = 0; c < T::kKChunks; ++c) {
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    qw[c][h] = __builtin_bit_cast(u32x4, qop[2 * c + h]);
+                }
+            }
+            rope_row_words<D>(qw, sm_rope, sm_rope + D / 2, lane);
+#pragma unroll
+            for (int c = 0; c < T::kKChunks; ++c) {
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    qop[2 * c + h] = __builtin_bit_cast(bf16x8, qw[c][h]);
+                }
+            }
+        }
+    };
 
     // Softmax state: m_ref is this lane's head reference maximum (shared by the
     // four lanes of a head); scores are exponentiated against it. It is raised
@@ -614,6 +770,7 @@ __global__ __launch_bounds__(kDecThreads) void flash_decode_kernel(
             for (int r = 0; r + 1 < kRing; ++r) {
                 load(ring[r], k0 + min(t_first + r, last_tile) * kTileKeys);
             }
+            rope_q();   // behind the first tile loads
             for (int t = t_first;; t += kRing) {
                 bool done = false;
 #pragma unroll
@@ -646,6 +803,8 @@ __global__ __launch_bounds__(kDecThreads) void flash_decode_kernel(
         } else {
             stream.template operator()<false>();
         }
+    } else {
+        rope_q();
     }
 
     if (kAppend && virt) {
@@ -654,7 +813,8 @@ __global__ __launch_bounds__(kDecThreads) void flash_decode_kernel(
         const int64_t row  = static_cast<int64_t>(prow) * hkc + kvc;
         quantize_new_token<D>(vt, k_new + static_cast<int64_t>(kvc) * D,
                               v_new + static_cast<int64_t>(kvc) * D, k_w + row * D,
-                              v_w + row * D, ks_w + row, vs_w + row, lane, kvh == kvc * nqb);
+                              v_w + row * D, ks_w + row, vs_w + row, lane, kvh == kvc * nqb,
+                              kRope ? sm_rope : nullptr, kRope ? sm_rope + D / 2 : nullptr);
         process(vt, p_new, p_new + 1);
     }
 
@@ -761,6 +921,38 @@ __global__ __launch_bounds__(kDecThreads) void flash_decode_kernel(
             part_l[slot]       = l_run;
         }
     }
+}
+
+template <int D, bool kAppend, bool kPaged>
+__global__ __launch_bounds__(kDecThreads) void flash_decode_kernel(
+    const uint16_t* __restrict__ q, const uint8_t* __restrict__ k,
+    const uint8_t* __restrict__ v, const float* __restrict__ ks,
+    const float* __restrict__ vs, float* __restrict__ partial, int num_splits,
+    const int* __restrict__ cache_len, int hq, int hkv, float scale_log2,
+    const uint16_t* __restrict__ k_new, const uint16_t* __restrict__ v_new,
+    uint8_t* k_w, uint8_t* v_w, float* ks_w, float* vs_w,
+    const int* __restrict__ block_table, int block_shift, int kvg, int nqb) {
+    decode_body<D, kAppend, kPaged, false>(q, k, v, ks, vs, partial, num_splits, cache_len, hq,
+                                           hkv, scale_log2, k_new, v_new, k_w, v_w, ks_w, vs_w,
+                                           block_table, block_shift, kvg, nqb, nullptr,
+                                           nullptr);
+}
+
+// The decode step with RoPE fused: rope of q and of the appended k row, the
+// append, and the split partials (the merge kernel follows as usual).
+template <int D, bool kPaged>
+__global__ __launch_bounds__(kDecThreads) void flash_decode_rope_kernel(
+    const uint16_t* __restrict__ q, const uint8_t* __restrict__ k,
+    const uint8_t* __restrict__ v, const float* __restrict__ ks,
+    const float* __restrict__ vs, float* __restrict__ partial, int num_splits,
+    const int* __restrict__ cache_len, int hq, int hkv, float scale_log2,
+    const uint16_t* __restrict__ k_new, const uint16_t* __restrict__ v_new,
+    uint8_t* k_w, uint8_t* v_w, float* ks_w, float* vs_w,
+    const int* __restrict__ block_table, int block_shift, int kvg, int nqb,
+    const int* __restrict__ positions, const float* __restrict__ inv_freq) {
+    decode_body<D, true, kPaged, true>(q, k, v, ks, vs, partial, num_splits, cache_len, hq, hkv,
+                                       scale_log2, k_new, v_new, k_w, v_w, ks_w, vs_w,
+                                       block_table, block_shift, kvg, nqb, positions, inv_freq);
 }
 
 // One workgroup per (q head, 16-wide slice of head_dim): merges the n_eff
@@ -1183,7 +1375,7 @@ hipError_t launch_decode(uint16_t* out, const uint16_t* q, const uint8_t* k,
                          int hq, int hkv, float scale, const uint16_t* k_new,
                          const uint16_t* v_new, uint8_t* k_w, uint8_t* v_w, float* ks_w,
                          float* vs_w, const int* block_table, int block_shift,
-                         hipStream_t stream) {
+                         hipStream_t stream, const int* positions, const float* inv_freq) {
     int        cus = 0;
     hipError_t ce  = device_cu_count(&cus);
     if (ce != hipSuccess) {
@@ -1197,7 +1389,15 @@ hipError_t launch_decode(uint16_t* out, const uint16_t* q, const uint8_t* k,
     const int  kvg   = dec_group_kv(num_splits, hkv_v, cus);
     const int  n_wgs = dec_workgroups(num_splits, hkv_v, kvg);
     const dim3 grid(static_cast<unsigned>(n_wgs));
-    if (k_new != nullptr) {
+    if (positions != nullptr) {
+        if (k_new == nullptr || inv_freq == nullptr) {
+            return hipErrorInvalidValue;
+        }
+        hipLaunchKernelGGL((flash_decode_rope_kernel<D, kPaged>), grid, dim3(kDecThreads), 0,
+                           stream, q, k, v, ks, vs, partial, num_splits, cache_len, hq, hkv_v,
+                           scale * kLog2e, k_new, v_new, k_w, v_w, ks_w, vs_w, block_table,
+                           block_shift, kvg, nqb, positions, inv_freq);
+    } else if (k_new != nullptr) {
         hipLaunchKernelGGL((flash_decode_kernel<D, true, kPaged>), grid, dim3(kDecThreads), 0,
                            stream, q, k, v, ks, vs, partial, num_splits, cache_len, hq, hkv_v,
                            scale * kLog2e, k_new, v_new, k_w, v_w, ks_w, vs_w, block_table,
@@ -1273,7 +1473,7 @@ hipError_t flash_decode_launch(uint16_t* out, const uint16_t* q,
                                hipStream_t stream, const uint16_t* k_new,
                                const uint16_t* v_new, uint8_t* k_w, uint8_t* v_w,
                                float* ks_w, float* vs_w, const int* block_table,
-                               int block_shift) {
+                               int block_shift, const int* positions, const float* inv_freq) {
     const bool paged = block_table != nullptr;
     switch (head_dim) {
 #define RTH_DEC_CASE(DD)                                                                      \
@@ -1281,11 +1481,13 @@ hipError_t flash_decode_launch(uint16_t* out, const uint16_t* q,
         return paged ? launch_decode<DD, true>(out, q, k, v, k_scale, v_scale, partial,       \
                                                num_splits, cache_len, num_q_heads,            \
                                                num_kv_heads, scale, k_new, v_new, k_w, v_w,   \
-                                               ks_w, vs_w, block_table, block_shift, stream)  \
+                                               ks_w, vs_w, block_table, block_shift, stream,  \
+                                               positions, inv_freq)                           \
                      : launch_decode<DD, false>(out, q, k, v, k_scale, v_scale, partial,      \
                                                 num_splits, cache_len, num_q_heads,           \
                                                 num_kv_heads, scale, k_new, v_new, k_w, v_w,  \
-                                                ks_w, vs_w, nullptr, 0, stream);
+                                                ks_w, vs_w, nullptr, 0, stream, positions,    \
+                                                inv_freq);
         RTH_DEC_CASE(64)
         RTH_DEC_CASE(128)
         RTH_DEC_CASE(256)
