@@ -170,6 +170,9 @@ def bench_decode(torch, R, args, stream):
     # rope_bf16 + append + run (4). One 128-step graph each, replayed twice
     # after one warmup replay; rope_bf16 rotates the stored q/k in place.
     inv = (5e5 ** (-torch.arange(0, d, 2, dtype=torch.float64, device=dev) / d)).float()
+    qg = torch.randn((d,), generator=gen, device=dev).to(torch.bfloat16)
+    kg = torch.randn((d,), generator=gen, device=dev).to(torch.bfloat16)
+    eps = 1e-6
     torch.cuda.synchronize()
 
     def run_rope_steps(mode, n_steps):
@@ -181,6 +184,19 @@ def bench_decode(torch, R, args, stream):
                 elif mode == "rope+fused":
                     R.rope_bf16(q, k, pos, inv, 1, hq, hkv, d)
                     backend.run_decode_append(o, q, view, k, v, pos)
+                elif mode == "qwen_fused":
+                    backend.run_decode_qk_norm_rope_append(o, q, view, k, v, qg, kg, eps, pos,
+                                                           inv, pos)
+                elif mode == "qwen_three":
+                    R.qk_norm_rope_append_fp8(q, view.k, view.v, view.k_scale, view.v_scale, k,
+                                              v, qg, kg, eps, pos, inv, pos, 1, hq, hkv, d)
+                    backend.run(o, q, view, 1, pos)
+                elif mode == "qwen_reference":
+                    R.rmsnorm_bf16(q, q, qg, hq, d, eps)
+                    R.rmsnorm_bf16(k, k, kg, hkv, d, eps)
+                    R.rope_bf16(q, k, pos, inv, 1, hq, hkv, d)
+                    cache.append(l, k, v, 1, pos)
+                    backend.run(o, q, view, 1, pos)
                 else:
                     R.rope_bf16(q, k, pos, inv, 1, hq, hkv, d)
                     cache.append(l, k, v, 1, pos)
@@ -189,7 +205,8 @@ def bench_decode(torch, R, args, stream):
         R.advance_position(pos, -n_steps)
 
     rope_ms = {}
-    for mode in ("fused", "rope+fused", "reference"):
+    for mode in ("fused", "rope+fused", "reference", "qwen_fused", "qwen_three",
+                 "qwen_reference"):
         g = torch.cuda.CUDAGraph()
         with torch.cuda.graph(g, stream=stream):
             run_rope_steps(mode, GRAPH_STEPS)
@@ -651,6 +668,17 @@ def main() -> int:
                         "rth_attn_decode_rope_append_split (2 kernels per layer) vs rope_bf16 + "
                         "the fused append/decode (3) vs rope_bf16 + append + run (4, the "
                         "reference's order); 128-step graphs",
+        },
+        "decode_step_qk_norm_rope": {
+            "unit": "ms/step (28 layers)",
+            "fused": round(dec["rope_ms_per_step"]["qwen_fused"], 4),
+            "qk_norm_rope_append_then_run": round(dec["rope_ms_per_step"]["qwen_three"], 4),
+            "reference_order": round(dec["rope_ms_per_step"]["qwen_reference"], 4),
+            "workload": "the same steps in Qwen3's order (per-head RMSNorm of q and k, RoPE, "
+                        "append, run; qwen3.cu:189-202): "
+                        "rth_attn_decode_qk_norm_rope_append_split (2 kernels per layer) vs "
+                        "rth_qk_norm_rope_append_fp8 + run (3) vs rmsnorm x2 + rope + append + "
+                        "run (6); 24Q/8KV head shape as above",
         },
         "cpu_baseline": cpu,
     }

@@ -244,6 +244,26 @@ int rth_attn_decode_rope_append_split_paged(uint16_t* out, const uint16_t* q, ui
                                             const int* cache_len, int num_q_heads,
                                             int num_kv_heads, int head_dim, float scale,
                                             void* stream);
+/* No counterpart in the reference: the Qwen3 decode step,
+ * rmsnorm_bf16_forward(q, q_norm) and (k, k_norm) per head -> rope_bf16 ->
+ * KVCache::append -> run (reference src/model/supported/llama/
+ * qwen3.cu:189-202), in the two launches of rth_attn_decode_append_split.
+ * q and k_new are read only; cache bytes and output are bit-identical to
+ * rth_qk_norm_rope_append_fp8 followed by rth_attn_decode_split. Shapes as
+ * rth_attn_decode_rope_append_split. */
+int rth_attn_decode_qk_norm_rope_append_split(
+    uint16_t* out, const uint16_t* q, uint8_t* k_cache, uint8_t* v_cache, float* k_scale,
+    float* v_scale, const uint16_t* k_new, const uint16_t* v_new, const uint16_t* q_norm,
+    const uint16_t* k_norm, float eps, const int* positions, const float* inv_freq,
+    float* partial, int num_splits, const int* cache_len, int num_q_heads, int num_kv_heads,
+    int head_dim, float scale, void* stream);
+int rth_attn_decode_qk_norm_rope_append_split_paged(
+    uint16_t* out, const uint16_t* q, uint8_t* k_cache, uint8_t* v_cache, float* k_scale,
+    float* v_scale, const int* block_table, int block_size, const uint16_t* k_new,
+    const uint16_t* v_new, const uint16_t* q_norm, const uint16_t* k_norm, float eps,
+    const int* positions, const float* inv_freq, float* partial, int num_splits,
+    const int* cache_len, int num_q_heads, int num_kv_heads, int head_dim, float scale,
+    void* stream);
 int rth_attn_prefill_paged(uint16_t* out, const uint16_t* q, const uint8_t* k,
                            const uint8_t* v, const float* k_scale, const float* v_scale,
                            const int* block_table, int block_size, int n_new,

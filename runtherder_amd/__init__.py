@@ -25,6 +25,7 @@ from .ops import (  # noqa: F401
     default_num_splits,
     flash_decode_append_split_bf16,
     flash_decode_rope_append_split_bf16,
+    flash_decode_qk_norm_rope_append_split_bf16,
     flash_decode_split_bf16,
     flash_decode_split_bf16_noalloc,
     flash_prefill_bf16,

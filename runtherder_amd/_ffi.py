@@ -56,6 +56,14 @@ _SIGNATURES = {
     "rth_attn_decode_rope_append_split_paged": (_c_int, [_vp] * 7 + [_c_int] + [_vp] * 5 +
                                                 [_c_int, _vp, _c_int, _c_int, _c_int,
                                                  ctypes.c_float, _vp]),
+    "rth_attn_decode_qk_norm_rope_append_split": (_c_int, [_vp] * 10 + [ctypes.c_float] +
+                                                  [_vp] * 3 + [_c_int, _vp, _c_int, _c_int,
+                                                               _c_int, ctypes.c_float, _vp]),
+    "rth_attn_decode_qk_norm_rope_append_split_paged": (_c_int, [_vp] * 7 + [_c_int] +
+                                                        [_vp] * 4 + [ctypes.c_float] +
+                                                        [_vp] * 3 +
+                                                        [_c_int, _vp, _c_int, _c_int, _c_int,
+                                                         ctypes.c_float, _vp]),
     "rth_attn_prefill_paged": (_c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_int, _c_int, _vp,
                                         _c_int, _c_int, _c_int, ctypes.c_float, _vp]),
 }

@@ -386,6 +386,54 @@ int rth_attn_decode_rope_append_split_paged(uint16_t* out, const uint16_t* q, ui
                      "rth_attn_decode_rope_append_split");
 }
 
+int rth_attn_decode_qk_norm_rope_append_split(
+    uint16_t* out, const uint16_t* q, uint8_t* k_cache, uint8_t* v_cache, float* k_scale,
+    float* v_scale, const uint16_t* k_new, const uint16_t* v_new, const uint16_t* q_norm,
+    const uint16_t* k_norm, float eps, const int* positions, const float* inv_freq,
+    float* partial, int num_splits, const int* cache_len, int num_q_heads, int num_kv_heads,
+    int head_dim, float scale, void* stream) {
+    return rth_attn_decode_qk_norm_rope_append_split_paged(
+        out, q, k_cache, v_cache, k_scale, v_scale, nullptr, 0, k_new, v_new, q_norm, k_norm,
+        eps, positions, inv_freq, partial, num_splits, cache_len, num_q_heads, num_kv_heads,
+        head_dim, scale, stream);
+}
+
+int rth_attn_decode_qk_norm_rope_append_split_paged(
+    uint16_t* out, const uint16_t* q, uint8_t* k_cache, uint8_t* v_cache, float* k_scale,
+    float* v_scale, const int* block_table, int block_size, const uint16_t* k_new,
+    const uint16_t* v_new, const uint16_t* q_norm, const uint16_t* k_norm, float eps,
+    const int* positions, const float* inv_freq, float* partial, int num_splits,
+    const int* cache_len, int num_q_heads, int num_kv_heads, int head_dim, float scale,
+    void* stream) {
+    if (int rc = check_attn(out, q, k_cache, v_cache, k_scale, v_scale, cache_len)) {
+        return rc;
+    }
+    int shift = 0;
+    if (block_table != nullptr) {
+        RTH_PAGED_ARGS(block_table, block_size, paged_shift);
+        shift = paged_shift;
+    }
+    RTH_REQUIRE(k_new != nullptr && v_new != nullptr, "k_new and v_new must not be null");
+    RTH_REQUIRE(q_norm != nullptr && k_norm != nullptr, "q_norm and k_norm must not be null");
+    RTH_REQUIRE(positions != nullptr && inv_freq != nullptr,
+                "positions and inv_freq must not be null");
+    RTH_REQUIRE(num_splits >= 1 && num_splits <= 65536, "num_splits must be in [1, 65536]");
+    if (int rc = check_heads(num_q_heads, num_kv_heads)) {
+        return rc;
+    }
+    RTH_REQUIRE(rth::decode_mfma_supported(num_q_heads, num_kv_heads, head_dim),
+                "the q/k-norm RoPE decode step supports head_dim 64, 128, 256 with GQA groups "
+                "of 4-16 q heads or blocks of them (rth_decode_path)");
+    RTH_REQUIRE(partial != nullptr, "partial must not be null");
+    return check_hip(rth::flash_decode_launch(out, q, k_cache, v_cache, k_scale, v_scale,
+                                              partial, num_splits, cache_len, num_q_heads,
+                                              num_kv_heads, head_dim, scale, as_stream(stream),
+                                              k_new, v_new, k_cache, v_cache, k_scale, v_scale,
+                                              block_table, shift, positions, inv_freq, q_norm,
+                                              k_norm, eps),
+                     "rth_attn_decode_qk_norm_rope_append_split");
+}
+
 int rth_kv_append_fp8_paged(uint8_t* k_cache, uint8_t* v_cache, float* k_scale,
                             float* v_scale, const uint16_t* k, const uint16_t* v,
                             const int* at_pos, int n_new, int num_kv_heads, int head_dim,

@@ -44,6 +44,7 @@
 
 #include "device_common.hpp"
 #include "launch.hpp"
+#include "rmsnorm_row.hpp"
 
 namespace rth {
 namespace {
@@ -275,6 +276,33 @@ __host__ __device__ constexpr int dec_workgroups(int num_splits, int hkv, int kv
                      : (num_splits * hkv + kDecWaves - 1) / kDecWaves;
 }
 
+// Sum over aligned groups of N lanes (N a power of two <= 64); every lane of
+// a group ends with the group's sum. Each level adds the partner group's
+// partial to the lane's own, as the xor butterfly does (rms_butterfly), so
+// the sums are bit-identical to it.
+template <int N>
+__device__ __forceinline__ float group_sum(float v) {
+    if constexpr (N >= 2) {   // lanes xor 1
+        v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xF, 0xF, false));
+    }
+    if constexpr (N >= 4) {   // lanes xor 2
+        v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xF, 0xF, false));
+    }
+    if constexpr (N >= 8) {   // the other quad of the 8 (row_half_mirror)
+        v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x141, 0xF, 0xF, false));
+    }
+    if constexpr (N >= 16) {  // the other 8 of the row (row_mirror)
+        v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x140, 0xF, 0xF, false));
+    }
+    if constexpr (N >= 32) {
+        v = wave_xor_sum(v, 16);
+    }
+    if constexpr (N >= 64) {
+        v = wave_xor_sum(v, 32);
+    }
+    return v;
+}
+
 // Rotate-half RoPE of the bf16 words a lane holds of one head row (the q
 // load and new-token layout: chunk c, half h, word i = elements
 // 16g + 64c + 8h + 2i, +1), as rope_bf16 computes it (rope.hip): element d
@@ -365,7 +393,9 @@ __device__ __forceinline__ void quantize_new_token(TileRaw<D>& vt, const uint16_
                                                    uint8_t* kc_row, uint8_t* vc_row,
                                                    float* ks_slot, float* vs_slot, int lane,
                                                    bool write, const float* rc = nullptr,
-                                                   const float* rs = nullptr) {
+                                                   const float* rs = nullptr,
+                                                   const uint16_t* k_norm = nullptr,
+                                                   float eps = 0.0f) {
     using T     = DecTraits<D>;
     const int n = lane & 15;
     const int g = lane >> 4;
@@ -378,6 +408,27 @@ __device__ __forceinline__ void quantize_new_token(TileRaw<D>& vt, const uint16_
         for (int h = 0; h < 2; ++h) {
             kw[c][h] = (n == 0) ? *reinterpret_cast<const u32x4*>(kx + 16 * g + 64 * c + 8 * h)
                                 : u32x4{0u, 0u, 0u, 0u};
+        }
+    }
+    if (k_norm != nullptr) {
+        // RMSNorm of the row in rmsnorm_vec's order: lanes 0 .. D/8-1 hold
+        // one 16-byte vector each for the sum of squares.
+        constexpr int kL = D / 8;
+        u32x4 rv = {0u, 0u, 0u, 0u};
+        if (lane < kL) {
+            rv = *reinterpret_cast<const u32x4*>(kx + 8 * lane);
+        }
+        const float rrms = __builtin_bit_cast(
+            float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(
+                       int, rms_inverse(group_sum<kL>(sumsq8(rv, 0.0f)), D, eps))));
+#pragma unroll
+        for (int c = 0; c < T::kKChunks; ++c) {
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const u32x4 gw =
+                    *reinterpret_cast<const u32x4*>(k_norm + 16 * g + 64 * c + 8 * h);
+                kw[c][h] = scale8(kw[c][h], gw, rrms);
+            }
         }
     }
     if (rc != nullptr) {
@@ -483,7 +534,10 @@ __device__ __forceinline__ void quantize_new_token(TileRaw<D>& vt, const uint16_
 // kRope (with kAppend): q and the appended k row are rotated in registers by
 // the angles of positions[0] (rope_bf16's arithmetic, see rope_row_words);
 // each wave builds its own cos/sin table after issuing its first tile loads.
-template <int D, bool kAppend, bool kPaged, bool kRope>
+// kNorm (with kRope): before the rotation, q rows and the appended k row
+// are RMS-normalized per head with the q_norm / k_norm gains (Qwen3's order,
+// rmsnorm_vec's arithmetic and reduction order).
+template <int D, bool kAppend, bool kPaged, bool kRope, bool kNorm = false>
 __device__ __forceinline__ void decode_body(
     const uint16_t* __restrict__ q, const uint8_t* __restrict__ k,
     const uint8_t* __restrict__ v, const float* __restrict__ ks,
@@ -492,9 +546,12 @@ __device__ __forceinline__ void decode_body(
     const uint16_t* __restrict__ k_new, const uint16_t* __restrict__ v_new,
     uint8_t* k_w, uint8_t* v_w, float* ks_w, float* vs_w,
     const int* __restrict__ block_table, int block_shift, int kvg, int nqb,
-    const int* __restrict__ positions, const float* __restrict__ inv_freq) {
+    const int* __restrict__ positions, const float* __restrict__ inv_freq,
+    const uint16_t* __restrict__ q_norm = nullptr, const uint16_t* __restrict__ k_norm = nullptr,
+    float eps = 0.0f) {
     using T = DecTraits<D>;
     static_assert(!kRope || kAppend, "the RoPE variant is the fused decode step");
+    static_assert(!kNorm || kRope, "the q/k norm runs before the RoPE");
 
     __shared__ __attribute__((aligned(16))) float sm_sc[kDecWaves][64];
     __shared__ __attribute__((aligned(16))) float sm_o[kDecWaves][kMaxGroupD];
@@ -503,6 +560,8 @@ __device__ __forceinline__ void decode_body(
     // kRope: cos (first D/2) and sin (next D/2) of the RoPE angles, built by
     // wave 0 for the whole workgroup.
     __shared__ __attribute__((aligned(16))) float sm_rope[kMaxD];
+    // kNorm: the q_norm (first kMaxD) and k_norm gains, staged by wave 0.
+    __shared__ __attribute__((aligned(16))) uint16_t sm_gain[2 * kMaxD];
 
     const int G    = hq / hkv;
     const int tid  = static_cast<int>(threadIdx.x);
@@ -544,20 +603,36 @@ __device__ __forceinline__ void decode_body(
     // building the table later waits for nothing else in flight; every wave
     // passes exactly one workgroup barrier, the one after which wave 0's
     // table is complete (a wave without keys passes it here).
-    [[maybe_unused]] float rope_inv[kRopeIter] = {};
-    [[maybe_unused]] int   rope_pos            = 0;
+    [[maybe_unused]] float    rope_inv[kRopeIter] = {};
+    [[maybe_unused]] int      rope_pos            = 0;
+    [[maybe_unused]] uint32_t gain_q[kRopeIter]   = {};   // 2 bf16 per lane and step
+    [[maybe_unused]] uint32_t gain_k[kRopeIter]   = {};
     if constexpr (kRope) {
         rope_pos = *positions;
 #pragma unroll
         for (int j = 0; j < kRopeIter; ++j) {
             if (lane + j * kWave < D / 2) {
                 rope_inv[j] = inv_freq[lane + j * kWave];
+                if constexpr (kNorm) {
+                    gain_q[j] = reinterpret_cast<const uint32_t*>(q_norm)[lane + j * kWave];
+                    gain_k[j] = reinterpret_cast<const uint32_t*>(k_norm)[lane + j * kWave];
+                }
             }
         }
     }
     auto rope_sync = [&]() {
         if constexpr (kRope) {
             if (wave == 0) {
+                if constexpr (kNorm) {
+#pragma unroll
+                    for (int j = 0; j < kRopeIter; ++j) {
+                        if (lane + j * kWave < D / 2) {
+                            reinterpret_cast<uint32_t*>(sm_gain)[lane + j * kWave] = gain_q[j];
+                            reinterpret_cast<uint32_t*>(sm_gain + kMaxD)[lane + j * kWave] =
+                                gain_k[j];
+                        }
+                    }
+                }
                 rope_table_wave<D>(sm_rope, sm_rope + D / 2, rope_pos, rope_inv, lane);
             }
             __syncthreads();
@@ -603,6 +678,22 @@ __device__ __forceinline__ void decode_body(
             }
         }
     }
+    // kNorm: the q rows again in rmsnorm_vec's layout (D/8 lanes per row, one
+    // 16-byte vector each), for the per-row sums of squares; loaded here, with
+    // q, and used behind the first tile loads.
+    constexpr int kQnL    = D / 8;
+    constexpr int kQnRpp  = kWave / kQnL;                            // rows per load
+    constexpr int kQnRows = (kMaxGroupD / D < 16) ? kMaxGroupD / D : 16;
+    constexpr int kQnPass = (kQnRows + kQnRpp - 1) / kQnRpp;
+    [[maybe_unused]] u32x4 qn_raw[kQnPass];
+    if constexpr (kNorm) {
+#pragma unroll
+        for (int p = 0; p < kQnPass; ++p) {
+            const int r = min(p * kQnRpp + lane / kQnL, G - 1);
+            qn_raw[p]   = *reinterpret_cast<const u32x4*>(
+                q + static_cast<int64_t>(kvh * G + r) * D + 8 * (lane % kQnL));
+        }
+    }
 
     f32x4 oacc[T::kOMfma];
 #pragma unroll
@@ -617,14 +708,8 @@ __device__ __forceinline__ void decode_body(
     // ring), where the table is built before any tile registers are live
     // (behind them its double-precision sincos spilled).
     constexpr bool kTableFirst = kRope && D == 256;
-    if constexpr (kTableFirst) {
-        rope_sync();
-    }
-    auto rope_q = [&]() {
+    auto rope_xform = [&]() {
         if constexpr (kRope) {
-            if constexpr (!kTableFirst) {
-                rope_sync();
-            }
             u32x4 qw[T::kKChunks][2];
 #pragma unroll
             for (int c = 0; c < T::kKChunks; ++c) {
@@ -632,6 +717,34 @@ __device__ __forceinline__ void decode_body(
                 for (int h = 0; h < 2; ++h) {
                     qw[c][h] = __builtin_bit_cast(u32x4, qop[2 * c + h]);
                 }
+            }
+            if constexpr (kNorm) {
+                // Per-row 1/rms through this wave's sm_m row (free until the
+                // cooperative merge); padding columns (n >= G) hold head 0's
+                // q, so they take head 0's factor.
+#pragma unroll
+                for (int p = 0; p < kQnPass; ++p) {
+                    if (p * kQnRpp < G) {   // passes holding real rows only
+                        const float rr =
+                            rms_inverse(group_sum<kQnL>(sumsq8(qn_raw[p], 0.0f)), D, eps);
+                        const int r = p * kQnRpp + lane / kQnL;
+                        if (lane % kQnL == 0 && r < kQnRows) {
+                            sm_m[wave][r] = rr;
+                        }
+                    }
+                }
+                __builtin_amdgcn_wave_barrier();
+                const float rrms = sm_m[wave][n < G ? n : 0];
+#pragma unroll
+                for (int c = 0; c < T::kKChunks; ++c) {
+#pragma unroll
+                    for (int h = 0; h < 2; ++h) {
+                        const u32x4 gw = *reinterpret_cast<const u32x4*>(sm_gain + 16 * g +
+                                                                         64 * c + 8 * h);
+                        qw[c][h] = scale8(qw[c][h], gw, rrms);
+                    }
+                }
+                __builtin_amdgcn_wave_barrier();
             }
             rope_row_words<D>(qw, sm_rope, sm_rope + D / 2, lane);
 #pragma unroll
@@ -649,6 +762,19 @@ __device__ __forceinline__ void decode_body(
     // only when some score exceeds it by more than 2^kLazy, so the usual tile
     // needs no cross-lane step and no accumulator rescale. Exact: every p and
     // l use the same reference, and p <= 2^kLazy keeps them in range.
+    // q transform point: here for head_dim 256, else behind the first tile
+    // loads (rope_q, called once per wave).
+    if constexpr (kTableFirst) {
+        rope_sync();
+        rope_xform();
+    }
+    auto rope_q = [&]() {
+        if constexpr (kRope && !kTableFirst) {
+            rope_sync();
+            rope_xform();
+        }
+    };
+
     constexpr float kLazy = 8.0f;
     auto process = [&](const TileRaw<D>& cur, const int kb, const int klim) {
         sm_sc[wave][lane] = cur.sc;
@@ -814,7 +940,8 @@ __device__ __forceinline__ void decode_body(
         quantize_new_token<D>(vt, k_new + static_cast<int64_t>(kvc) * D,
                               v_new + static_cast<int64_t>(kvc) * D, k_w + row * D,
                               v_w + row * D, ks_w + row, vs_w + row, lane, kvh == kvc * nqb,
-                              kRope ? sm_rope : nullptr, kRope ? sm_rope + D / 2 : nullptr);
+                              kRope ? sm_rope : nullptr, kRope ? sm_rope + D / 2 : nullptr,
+                              kNorm ? sm_gain + kMaxD : nullptr, eps);
         process(vt, p_new, p_new + 1);
     }
 
@@ -953,6 +1080,25 @@ __global__ __launch_bounds__(kDecThreads) void flash_decode_rope_kernel(
     decode_body<D, true, kPaged, true>(q, k, v, ks, vs, partial, num_splits, cache_len, hq, hkv,
                                        scale_log2, k_new, v_new, k_w, v_w, ks_w, vs_w,
                                        block_table, block_shift, kvg, nqb, positions, inv_freq);
+}
+
+// The Qwen3 decode step: per-head RMSNorm of q and of the appended k row,
+// then RoPE, the append and the split partials.
+template <int D, bool kPaged>
+__global__ __launch_bounds__(kDecThreads) void flash_decode_qk_norm_rope_kernel(
+    const uint16_t* __restrict__ q, const uint8_t* __restrict__ k,
+    const uint8_t* __restrict__ v, const float* __restrict__ ks,
+    const float* __restrict__ vs, float* __restrict__ partial, int num_splits,
+    const int* __restrict__ cache_len, int hq, int hkv, float scale_log2,
+    const uint16_t* __restrict__ k_new, const uint16_t* __restrict__ v_new,
+    uint8_t* k_w, uint8_t* v_w, float* ks_w, float* vs_w,
+    const int* __restrict__ block_table, int block_shift, int kvg, int nqb,
+    const int* __restrict__ positions, const float* __restrict__ inv_freq,
+    const uint16_t* __restrict__ q_norm, const uint16_t* __restrict__ k_norm, float eps) {
+    decode_body<D, true, kPaged, true, true>(q, k, v, ks, vs, partial, num_splits, cache_len, hq,
+                                             hkv, scale_log2, k_new, v_new, k_w, v_w, ks_w, vs_w,
+                                             block_table, block_shift, kvg, nqb, positions,
+                                             inv_freq, q_norm, k_norm, eps);
 }
 
 // One workgroup per (q head, 16-wide slice of head_dim): merges the n_eff
@@ -1101,30 +1247,6 @@ struct ValuTraits {
     static constexpr int kRing = 4;              // steps in flight per wave
 };
 
-// Sum over aligned groups of N lanes (N a power of two <= 64); every lane of
-// a group ends with the group's sum.
-template <int N>
-__device__ __forceinline__ float group_sum(float v) {
-    if constexpr (N >= 2) {   // lanes xor 1
-        v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xF, 0xF, false));
-    }
-    if constexpr (N >= 4) {   // lanes xor 2
-        v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xF, 0xF, false));
-    }
-    if constexpr (N >= 8) {   // the other quad of the 8 (row_half_mirror)
-        v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x141, 0xF, 0xF, false));
-    }
-    if constexpr (N >= 16) {  // the other 8 of the row (row_mirror)
-        v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x140, 0xF, 0xF, false));
-    }
-    if constexpr (N >= 32) {
-        v = wave_xor_sum(v, 16);
-    }
-    if constexpr (N >= 64) {
-        v = wave_xor_sum(v, 32);
-    }
-    return v;
-}
 
 template <int D>
 struct ValuStep {
@@ -1375,7 +1497,8 @@ hipError_t launch_decode(uint16_t* out, const uint16_t* q, const uint8_t* k,
                          int hq, int hkv, float scale, const uint16_t* k_new,
                          const uint16_t* v_new, uint8_t* k_w, uint8_t* v_w, float* ks_w,
                          float* vs_w, const int* block_table, int block_shift,
-                         hipStream_t stream, const int* positions, const float* inv_freq) {
+                         hipStream_t stream, const int* positions, const float* inv_freq,
+                         const uint16_t* q_norm, const uint16_t* k_norm, float eps) {
     int        cus = 0;
     hipError_t ce  = device_cu_count(&cus);
     if (ce != hipSuccess) {
@@ -1389,7 +1512,17 @@ hipError_t launch_decode(uint16_t* out, const uint16_t* q, const uint8_t* k,
     const int  kvg   = dec_group_kv(num_splits, hkv_v, cus);
     const int  n_wgs = dec_workgroups(num_splits, hkv_v, kvg);
     const dim3 grid(static_cast<unsigned>(n_wgs));
-    if (positions != nullptr) {
+    if (q_norm != nullptr) {
+        if (k_new == nullptr || inv_freq == nullptr || positions == nullptr ||
+            k_norm == nullptr) {
+            return hipErrorInvalidValue;
+        }
+        hipLaunchKernelGGL((flash_decode_qk_norm_rope_kernel<D, kPaged>), grid,
+                           dim3(kDecThreads), 0, stream, q, k, v, ks, vs, partial, num_splits,
+                           cache_len, hq, hkv_v, scale * kLog2e, k_new, v_new, k_w, v_w, ks_w,
+                           vs_w, block_table, block_shift, kvg, nqb, positions, inv_freq,
+                           q_norm, k_norm, eps);
+    } else if (positions != nullptr) {
         if (k_new == nullptr || inv_freq == nullptr) {
             return hipErrorInvalidValue;
         }
@@ -1473,7 +1606,8 @@ hipError_t flash_decode_launch(uint16_t* out, const uint16_t* q,
                                hipStream_t stream, const uint16_t* k_new,
                                const uint16_t* v_new, uint8_t* k_w, uint8_t* v_w,
                                float* ks_w, float* vs_w, const int* block_table,
-                               int block_shift, const int* positions, const float* inv_freq) {
+                               int block_shift, const int* positions, const float* inv_freq,
+                               const uint16_t* q_norm, const uint16_t* k_norm, float eps) {
     const bool paged = block_table != nullptr;
     switch (head_dim) {
 #define RTH_DEC_CASE(DD)                                                                      \
@@ -1482,12 +1616,12 @@ hipError_t flash_decode_launch(uint16_t* out, const uint16_t* q,
                                                num_splits, cache_len, num_q_heads,            \
                                                num_kv_heads, scale, k_new, v_new, k_w, v_w,   \
                                                ks_w, vs_w, block_table, block_shift, stream,  \
-                                               positions, inv_freq)                           \
+                                               positions, inv_freq, q_norm, k_norm, eps)      \
                      : launch_decode<DD, false>(out, q, k, v, k_scale, v_scale, partial,      \
                                                 num_splits, cache_len, num_q_heads,           \
                                                 num_kv_heads, scale, k_new, v_new, k_w, v_w,  \
                                                 ks_w, vs_w, nullptr, 0, stream, positions,    \
-                                                inv_freq);
+                                                inv_freq, q_norm, k_norm, eps);
         RTH_DEC_CASE(64)
         RTH_DEC_CASE(128)
         RTH_DEC_CASE(256)

@@ -56,7 +56,9 @@ hipError_t flash_decode_launch(uint16_t* out, const uint16_t* q,
                                uint8_t* v_w = nullptr, float* ks_w = nullptr,
                                float* vs_w = nullptr, const int* block_table = nullptr,
                                int block_shift = 0, const int* positions = nullptr,
-                               const float* inv_freq = nullptr);
+                               const float* inv_freq = nullptr,
+                               const uint16_t* q_norm = nullptr,
+                               const uint16_t* k_norm = nullptr, float eps = 0.0f);
 
 // The VALU split kernel + merge: head_dim in {32, 64, 128, 256, 512}, any
 // GQA group (no paging, no fused append). The decode entry points use it for

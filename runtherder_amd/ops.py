@@ -153,6 +153,28 @@ def flash_decode_rope_append_split_bf16(out, q, k_cache, v_cache, k_scale, v_sca
               float(scale), _stream(stream))
 
 
+def flash_decode_qk_norm_rope_append_split_bf16(out, q, k_cache, v_cache, k_scale, v_scale,
+                                                k_new, v_new, q_norm, k_norm, eps, positions,
+                                                inv_freq, partial, num_splits, cache_len,
+                                                num_q_heads, num_kv_heads, head_dim, scale,
+                                                stream=None):
+    """The Qwen3 decode step (per-head RMSNorm of q and k, RoPE, append, run)
+    in one call (no reference counterpart; replaces reference
+    src/model/supported/llama/qwen3.cu:189-202). q and k_new are read only."""
+    _need(out, torch.bfloat16, "out"); _need(q, torch.bfloat16, "q")
+    _need(k_cache, torch.uint8, "k_cache"); _need(v_cache, torch.uint8, "v_cache")
+    _need(k_scale, torch.float32, "k_scale"); _need(v_scale, torch.float32, "v_scale")
+    _need(k_new, torch.bfloat16, "k_new"); _need(v_new, torch.bfloat16, "v_new")
+    _need(q_norm, torch.bfloat16, "q_norm"); _need(k_norm, torch.bfloat16, "k_norm")
+    _need(positions, torch.int32, "positions"); _need(inv_freq, torch.float32, "inv_freq")
+    _need(partial, torch.float32, "partial"); _need(cache_len, torch.int32, "cache_len")
+    _ffi.call("rth_attn_decode_qk_norm_rope_append_split", _p(out), _p(q), _p(k_cache),
+              _p(v_cache), _p(k_scale), _p(v_scale), _p(k_new), _p(v_new), _p(q_norm),
+              _p(k_norm), float(eps), _p(positions), _p(inv_freq), _p(partial), num_splits,
+              _p(cache_len), num_q_heads, num_kv_heads, head_dim, float(scale),
+              _stream(stream))
+
+
 def flash_prefill_bf16(out, q, k, v, k_scale, v_scale, n_new, cache_len, num_q_heads,
                        num_kv_heads, head_dim, scale, stream=None):
     """reference include/runtherder/kernels/flash_prefill.cuh:26-39"""
@@ -436,6 +458,25 @@ class AdaptiveAttention(AttentionBackend):
                                             v_new, positions, inv_freq, self.partial,
                                             self.num_splits, cache_len, c.num_q_heads,
                                             c.num_kv_heads, c.head_dim, c.scale, stream)
+
+
+    def run_decode_qk_norm_rope_append(self, out, q, kv, k_new, v_new, q_norm, k_norm, eps,
+                                       positions, inv_freq, cache_len, stream=None):
+        """Qwen3 order: per-head RMSNorm(q, q_norm) and (k_new, k_norm), RoPE,
+        KVCache.append and run(..., n_new=1) in one call; q and k_new read only."""
+        c = self.config
+        if kv.block_table is not None:
+            _ffi.call("rth_attn_decode_qk_norm_rope_append_split_paged", _p(out), _p(q),
+                      _p(kv.k), _p(kv.v), _p(kv.k_scale), _p(kv.v_scale), _p(kv.block_table),
+                      kv.block_size, _p(k_new), _p(v_new), _p(q_norm), _p(k_norm), float(eps),
+                      _p(positions), _p(inv_freq), _p(self.partial), self.num_splits,
+                      _p(cache_len), c.num_q_heads, c.num_kv_heads, c.head_dim, float(c.scale),
+                      _stream(stream))
+            return
+        flash_decode_qk_norm_rope_append_split_bf16(
+            out, q, kv.k, kv.v, kv.k_scale, kv.v_scale, k_new, v_new, q_norm, k_norm, eps,
+            positions, inv_freq, self.partial, self.num_splits, cache_len, c.num_q_heads,
+            c.num_kv_heads, c.head_dim, c.scale, stream)
 
 
 class NaiveAttention(AttentionBackend):

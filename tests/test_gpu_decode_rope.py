@@ -145,3 +145,101 @@ def test_rope_decode_step_rejects_valu_shapes():
             zs.clone(), zb, zb.clone(), int_dev(0), f32_dev(np.ones(d // 2, np.float32)),
             R.new_flash_split_scratch(hq, d, 4), 4, int_dev(3), hq, hkv, d, 0.1)
     assert "RoPE decode step" in str(e.value)
+
+
+@pytest.mark.parametrize("cache_len,hq,hkv,d,splits,pos", [
+    (8195, 32, 8, 128, None, 8195),    # Qwen3-8B shape
+    (0, 32, 8, 128, None, 0),
+    (700, 16, 4, 64, 16, 700),
+    (300, 16, 4, 256, 8, 300),
+    (2000, 64, 2, 128, 64, 2000),      # q blocks of 16
+    (130, 16, 1, 256, 8, 130),
+])
+def test_qk_norm_rope_decode_step_equals_unfused(cache_len, hq, hkv, d, splits, pos):
+    """Qwen3 order (qwen3.cu:189-202): rmsnorm per head of q and k, RoPE,
+    append, decode. Reference: rth_rmsnorm_bf16 and rth_rope_bf16 on copies,
+    then the fused append + decode on the transformed rows."""
+    eps = 1e-6
+    total = cache_len + 1
+    splits = splits or R.default_num_splits(hkv)
+    scale = np.float32(1.0 / np.sqrt(d))
+    k8, ks = O.quantize_kv_fp8(O.normal_bf16((total * hkv, d), 7100 + cache_len), d)
+    v8, vs = O.quantize_kv_fp8(O.normal_bf16((total * hkv, d), 8100 + cache_len), d)
+    rows = slice(cache_len * hkv, total * hkv)
+    for a in (k8, v8, ks, vs):
+        a[rows] = 0
+    q = O.normal_bf16((hq, d), 110 + hq + d)
+    kn = O.normal_bf16((hkv, d), 210 + hkv + d)
+    vn = O.normal_bf16((hkv, d), 310 + hkv + d)
+    qg = O.normal_bf16((d,), 410 + d)
+    kg = O.normal_bf16((d,), 510 + d)
+    inv = inv_table(d, "plain")
+    posd, invd, cl = i32_dev(np.array([pos], np.int32)), f32_dev(inv), int_dev(cache_len)
+    qgd, kgd = bf16_dev(qg), bf16_dev(kg)
+
+    step(f"qk-norm rope decode step ctx={total} hq={hq} hkv={hkv} d={d} splits={splits}")
+    kc1, vc1, ks1, vs1 = u8_dev(k8), u8_dev(v8), f32_dev(ks), f32_dev(vs)
+    qd, knd = bf16_dev(q), bf16_dev(kn)
+    out1 = torch.empty((hq, d), dtype=torch.bfloat16, device=DEV)
+    R.flash_decode_qk_norm_rope_append_split_bf16(out1, qd, kc1, vc1, ks1, vs1, knd, bf16_dev(vn),
+                                                  qgd, kgd, eps, posd, invd,
+                                                  R.new_flash_split_scratch(hq, d, splits),
+                                                  splits, cl, hq, hkv, d, scale)
+
+    kc2, vc2, ks2, vs2 = u8_dev(k8), u8_dev(v8), f32_dev(ks), f32_dev(vs)
+    qr, knr = bf16_dev(q), bf16_dev(kn)
+    R.rmsnorm_bf16(qr, qr, qgd, hq, d, eps)
+    R.rmsnorm_bf16(knr, knr, kgd, hkv, d, eps)
+    R.rope_bf16(qr, knr, posd, invd, 1, hq, hkv, d)
+    out2 = torch.empty((hq, d), dtype=torch.bfloat16, device=DEV)
+    R.flash_decode_append_split_bf16(out2, qr, kc2, vc2, ks2, vs2, knr, bf16_dev(vn),
+                                     R.new_flash_split_scratch(hq, d, splits), splits, cl, hq,
+                                     hkv, d, scale)
+    sync()
+
+    assert np.array_equal(bf16_host(qd), q) and np.array_equal(bf16_host(knd), kn)
+    for a, b in ((kc1, kc2), (vc1, vc2)):
+        assert np.array_equal(a.cpu().numpy(), b.cpu().numpy())
+    for a, b in ((ks1, ks2), (vs1, vs2)):
+        assert np.array_equal(a.cpu().numpy().view(np.uint32), b.cpu().numpy().view(np.uint32))
+    got = bf16_host(out1)
+    assert np.array_equal(got, bf16_host(out2))
+
+    lanes = R.rmsnorm_lanes(d)
+    q_t = O.rope_apply_bf16(O.rmsnorm_bf16(q, qg, eps, lanes)[None], np.array([pos], np.int32),
+                            inv)[0]
+    k_t = O.rope_apply_bf16(O.rmsnorm_bf16(kn, kg, eps, lanes)[None],
+                            np.array([pos], np.int32), inv)[0]
+    assert np.array_equal(bf16_host(qr), q_t)
+    wk, wks = O.quantize_kv_fp8(k_t, d)
+    gk, gks = kc1.cpu().numpy(), ks1.cpu().numpy()
+    assert np.array_equal(gk[rows], wk)
+    assert np.array_equal(gks[rows].view(np.uint32), wks.view(np.uint32))
+    want = O.attention_f32(q_t, gk, vc1.cpu().numpy(), gks, vs1.cpu().numpy(), 1, cache_len,
+                           hq, hkv, d, scale, NTHREADS)
+    mx, mean = O.bf16_err(got, want[0])
+    assert mx <= MAX_ABS and mean <= MEAN_ABS, (mx, mean)
+
+
+def test_paged_qk_norm_rope_decode_step():
+    total, block, hq, hkv, d = 1500, 64, 32, 8, 128
+    eps, pos = 1e-6, 1499
+    cont, paged, bt, table, _, _ = make_pair(total - 1, hq, hkv, d, block, 77)
+    be = R.AdaptiveAttention(R.AttnConfig.for_heads(hq, hkv, d))
+    q = bf16_dev(O.normal_bf16((hq, d), 78))
+    kn, vn = bf16_dev(O.normal_bf16((hkv, d), 79)), bf16_dev(O.normal_bf16((hkv, d), 80))
+    qg, kg = bf16_dev(O.normal_bf16((d,), 81)), bf16_dev(O.normal_bf16((d,), 82))
+    posd, invd, cl = i32_dev(np.array([pos], np.int32)), f32_dev(inv_table(d, "plain")), \
+        int_dev(total - 1)
+    step("paged qk-norm rope decode step")
+    o_p = torch.empty((hq, d), dtype=torch.bfloat16, device=DEV)
+    o_c = torch.empty_like(o_p)
+    be.run_decode_qk_norm_rope_append(o_p, q, paged.view(0, bt), kn, vn, qg, kg, eps, posd, invd,
+                                      cl)
+    be.run_decode_qk_norm_rope_append(o_c, q, cont.view(0), kn, vn, qg, kg, eps, posd, invd, cl)
+    sync()
+    assert np.array_equal(bf16_host(o_p), bf16_host(o_c))
+    gk, _, gks, _ = gather(paged, table, total, block)
+    assert np.array_equal(gk, cont.k[0].cpu().numpy()[:total])
+    assert np.array_equal(gks.view(np.uint32),
+                          cont.k_scale[0].cpu().numpy()[:total].view(np.uint32))
