@@ -164,21 +164,48 @@ def bench_decode(torch, R, args, stream):
     value_gbs = total_bytes / (timed[True] * 1e-3) / 1e9
     unfused_gbs = total_bytes / (timed[False] * 1e-3) / 1e9
 
+    # Dominant kernels alone: one decode call (split kernel + merge kernel) per
+    # layer, rotating over the 28 layers (defeats the 256 MB Infinity Cache),
+    # captured back to back in a graph and timed with HIP events on its stream.
+    n_launch = L * 20
+    kgraph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(stream):
+        pos.fill_(depth)
+        torch.cuda.synchronize()
+        with torch.cuda.graph(kgraph, stream=stream):
+            for i in range(n_launch):
+                l = i % L
+                backend.run(out[0, l], qs[0, l], cache.view(l), 1, pos)
+        kgraph.replay()
+        torch.cuda.synchronize()
+        with EventTimer(torch, stream) as tk:
+            kgraph.replay()
+    torch.cuda.synchronize()
+    kern_us = tk.ms * 1e3 / n_launch
+    kbytes = decode_bytes(depth + 1, hq, hkv, d)
+    achieved = kbytes / (kern_us * 1e-6) / 1e9
+
     # The same steps with RoPE in them (the engine's per-layer sequence
     # rope -> append -> run): the fused RoPE entry (2 launches per layer),
     # rope_bf16 + the fused append/decode (3), and the reference's order
     # rope_bf16 + append + run (4). One 128-step graph each, replayed twice
-    # after one warmup replay; rope_bf16 rotates the stored q/k in place.
+    # after one warmup replay. Measured after the kernel loop above and on
+    # copies of q and k, which the unfused orders rotate (and normalize) in
+    # place.
     inv = (5e5 ** (-torch.arange(0, d, 2, dtype=torch.float64, device=dev) / d)).float()
     qg = torch.randn((d,), generator=gen, device=dev).to(torch.bfloat16)
     kg = torch.randn((d,), generator=gen, device=dev).to(torch.bfloat16)
     eps = 1e-6
     torch.cuda.synchronize()
 
+    with torch.cuda.stream(stream):
+        qs_r, ks_r = qs.clone(), ks.clone()
+    torch.cuda.synchronize()
+
     def run_rope_steps(mode, n_steps):
         for s in range(n_steps):
             for l in range(L):
-                q, k, v, o, view = qs[s, l], ks[s, l], vs[s, l], out[s, l], cache.view(l)
+                q, k, v, o, view = qs_r[s, l], ks_r[s, l], vs[s, l], out[s, l], cache.view(l)
                 if mode == "fused":
                     backend.run_decode_rope_append(o, q, view, k, v, pos, inv, pos)
                 elif mode == "rope+fused":
@@ -221,26 +248,6 @@ def bench_decode(torch, R, args, stream):
         rope_ms[mode] = t.ms / (2 * GRAPH_STEPS)
         del g
 
-    # Dominant kernels alone: one decode call (split kernel + merge kernel) per
-    # layer, rotating over the 28 layers (defeats the 256 MB Infinity Cache),
-    # captured back to back in a graph and timed with HIP events on its stream.
-    n_launch = L * 20
-    kgraph = torch.cuda.CUDAGraph()
-    with torch.cuda.stream(stream):
-        pos.fill_(depth)
-        torch.cuda.synchronize()
-        with torch.cuda.graph(kgraph, stream=stream):
-            for i in range(n_launch):
-                l = i % L
-                backend.run(out[0, l], qs[0, l], cache.view(l), 1, pos)
-        kgraph.replay()
-        torch.cuda.synchronize()
-        with EventTimer(torch, stream) as tk:
-            kgraph.replay()
-    torch.cuda.synchronize()
-    kern_us = tk.ms * 1e3 / n_launch
-    kbytes = decode_bytes(depth + 1, hq, hkv, d)
-    achieved = kbytes / (kern_us * 1e-6) / 1e9
     return {
         "value": value_gbs, "ms_per_step": ms_per_step, "steps": steps,
         "unfused_value": unfused_gbs, "unfused_ms_per_step": timed[False] / steps,
