@@ -243,3 +243,54 @@ def test_paged_qk_norm_rope_decode_step():
     assert np.array_equal(gk, cont.k[0].cpu().numpy()[:total])
     assert np.array_equal(gks.view(np.uint32),
                           cont.k_scale[0].cpu().numpy()[:total].view(np.uint32))
+
+
+def test_rope_decode_steps_in_a_graph():
+    """Four fused RoPE decode steps of one layer captured in a HIP graph with a
+    device-side position advance (rth_advance_position), replayed twice with
+    eager work in between: every replay's outputs and cache rows equal the
+    same steps run eagerly."""
+    hq, hkv, d, depth, steps = 24, 8, 128, 3000, 4
+    inv = f32_dev(inv_table(d, "llama3"))
+    k8, ks = O.quantize_kv_fp8(O.normal_bf16(((depth + steps) * hkv, d), 61), d)
+    v8, vs = O.quantize_kv_fp8(O.normal_bf16(((depth + steps) * hkv, d), 62), d)
+    q = bf16_dev(O.normal_bf16((steps, hq, d), 63))
+    kn = bf16_dev(O.normal_bf16((steps, hkv, d), 64))
+    vn = bf16_dev(O.normal_bf16((steps, hkv, d), 65))
+    splits = R.default_num_splits(hkv)
+    be = R.AdaptiveAttention(R.AttnConfig.for_heads(hq, hkv, d), splits)
+
+    def fresh():
+        return u8_dev(k8), u8_dev(v8), f32_dev(ks), f32_dev(vs)
+
+    def run(view_k, view_v, view_ks, view_vs, out, pos, stream=None):
+        for s in range(steps):
+            R.flash_decode_rope_append_split_bf16(out[s], q[s], view_k, view_v, view_ks, view_vs,
+                                                  kn[s], vn[s], pos, inv, be.partial, splits,
+                                                  pos, hq, hkv, d, be.config.scale, stream)
+            R.advance_position(pos, 1, stream)
+        R.advance_position(pos, -steps, stream)
+
+    step("rope decode steps, eager")
+    ek = fresh()
+    e_out = torch.empty((steps, hq, d), dtype=torch.bfloat16, device=DEV)
+    run(*ek, e_out, int_dev(depth))
+    sync()
+
+    gk = fresh()
+    g_out = torch.zeros_like(e_out)
+    g_pos = int_dev(depth)
+    stream = torch.cuda.Stream()
+    sync()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        run(*gk, g_out, g_pos, stream.cuda_stream)
+    for rep in range(2):
+        step(f"rope decode steps, graph replay {rep}")
+        g_out.zero_()
+        graph.replay()
+        sync()
+        assert np.array_equal(bf16_host(g_out), bf16_host(e_out))
+        for a, b in zip(gk, ek):
+            assert np.array_equal(a.cpu().numpy(), b.cpu().numpy())
+        torch.zeros((1 << 20,), device=DEV).sum().item()   # eager work between replays
