@@ -387,6 +387,9 @@ __device__ __forceinline__ void rope_table_wave(float* rc, float* rs, int pos,
 // The appended token's quantized K/V codes for one (kv head) unit, laid out
 // as the tile registers of key 0 of a tile after k_rows_to_mfma, plus the
 // scales. rc != nullptr: K is rotated first (RoPE, see rope_row_words).
+// pk / pv != nullptr: the row's words were loaded at kernel start (every lane
+// loads its would-be words unconditionally; the n / g ownership selects stay
+// here), so the wave does not wait on them after the key stream.
 template <int D>
 __device__ __forceinline__ void quantize_new_token(TileRaw<D>& vt, const uint16_t* __restrict__ kx,
                                                    const uint16_t* __restrict__ vx,
@@ -395,7 +398,8 @@ __device__ __forceinline__ void quantize_new_token(TileRaw<D>& vt, const uint16_
                                                    bool write, const float* rc = nullptr,
                                                    const float* rs = nullptr,
                                                    const uint16_t* k_norm = nullptr,
-                                                   float eps = 0.0f) {
+                                                   float eps = 0.0f, const u32x4* pk = nullptr,
+                                                   const uint32_t* pv = nullptr) {
     using T     = DecTraits<D>;
     const int n = lane & 15;
     const int g = lane >> 4;
@@ -406,7 +410,8 @@ __device__ __forceinline__ void quantize_new_token(TileRaw<D>& vt, const uint16_
     for (int c = 0; c < T::kKChunks; ++c) {
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
-            kw[c][h] = (n == 0) ? *reinterpret_cast<const u32x4*>(kx + 16 * g + 64 * c + 8 * h)
+            kw[c][h] = (n == 0) ? (pk != nullptr ? pk[2 * c + h]
+                                                 : *reinterpret_cast<const u32x4*>(kx + 16 * g + 64 * c + 8 * h))
                                 : u32x4{0u, 0u, 0u, 0u};
         }
     }
@@ -451,7 +456,7 @@ __device__ __forceinline__ void quantize_new_token(TileRaw<D>& vt, const uint16_
     float         vmax = 0.0f;
 #pragma unroll
     for (int i = 0; i < kVW; ++i) {
-        vw[i] = (g == 0) ? *reinterpret_cast<const uint32_t*>(vx + T::kVBytes * n + 2 * i) : 0u;
+        vw[i] = (g == 0) ? (pv != nullptr ? pv[i] : *reinterpret_cast<const uint32_t*>(vx + T::kVBytes * n + 2 * i)) : 0u;
         vmax  = fmaxf(vmax, fabsf(__uint_as_float(vw[i] << 16)));
         vmax  = fmaxf(vmax, fabsf(__uint_as_float(vw[i] & 0xffff0000u)));
     }
@@ -644,6 +649,27 @@ __device__ __forceinline__ void decode_body(
     }
     const int kvc = kvh / nqb;   // cache kv head
     const int hkc = hkv / nqb;   // cache kv heads
+    // The appended row's bf16 words, issued before the stream (D <= 128: the
+    // 40 VGPRs they hold through the stream spill the D = 256 kernels). Plain
+    // loads, not loads inside the owner branch: a branch-merged load makes the
+    // compiler wait for every outstanding load at the merge.
+    [[maybe_unused]] u32x4    pre_k[DecTraits<D>::kKChunks * 2];
+    [[maybe_unused]] uint32_t pre_v[DecTraits<D>::kVBytes / 2];
+    if constexpr (kAppend && !kNorm && D <= 128) {
+        const uint16_t* kx = k_new + static_cast<int64_t>(kvc) * D;
+        const uint16_t* vx = v_new + static_cast<int64_t>(kvc) * D;
+#pragma unroll
+        for (int c = 0; c < DecTraits<D>::kKChunks; ++c) {
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                pre_k[2 * c + h] = *reinterpret_cast<const u32x4*>(kx + 16 * ((lane >> 4) & 3) + 64 * c + 8 * h);
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < DecTraits<D>::kVBytes / 2; ++i) {
+            pre_v[i] = *reinterpret_cast<const uint32_t*>(vx + DecTraits<D>::kVBytes * (lane & 15) + 2 * i);
+        }
+    }
     const int k0 = split_tile(pt, si) * kTileKeys;
     // With an append, the split holding the new key (the last one) reads
     // only the keys before it from the cache; one of its waves adds the new
@@ -941,7 +967,9 @@ __device__ __forceinline__ void decode_body(
                               v_new + static_cast<int64_t>(kvc) * D, k_w + row * D,
                               v_w + row * D, ks_w + row, vs_w + row, lane, kvh == kvc * nqb,
                               kRope ? sm_rope : nullptr, kRope ? sm_rope + D / 2 : nullptr,
-                              kNorm ? sm_gain + kMaxD : nullptr, eps);
+                              kNorm ? sm_gain + kMaxD : nullptr, eps,
+                              (kAppend && !kNorm && D <= 128) ? pre_k : nullptr,
+                              (kAppend && !kNorm && D <= 128) ? pre_v : nullptr);
         process(vt, p_new, p_new + 1);
     }
 
