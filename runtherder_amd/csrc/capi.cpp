@@ -375,8 +375,9 @@ int rth_attn_decode_rope_append_split_paged(uint16_t* out, const uint16_t* q, ui
         return rc;
     }
     RTH_REQUIRE(rth::decode_mfma_supported(num_q_heads, num_kv_heads, head_dim),
-                "the RoPE decode step supports head_dim 64, 128, 256 with GQA groups of 4-16 q "
-                "heads or blocks of them (rth_decode_path)");
+                "the RoPE decode step supports head_dim 64, 128, 256 with GQA groups of up to "
+                "g = min(16, 2048 / head_dim) q heads, or groups in equal blocks of 4 to g "
+                "(rth_decode_path)");
     RTH_REQUIRE(partial != nullptr, "partial must not be null");
     return check_hip(rth::flash_decode_launch(out, q, k_cache, v_cache, k_scale, v_scale,
                                               partial, num_splits, cache_len, num_q_heads,
@@ -423,7 +424,8 @@ int rth_attn_decode_qk_norm_rope_append_split_paged(
     }
     RTH_REQUIRE(rth::decode_mfma_supported(num_q_heads, num_kv_heads, head_dim),
                 "the q/k-norm RoPE decode step supports head_dim 64, 128, 256 with GQA groups "
-                "of 4-16 q heads or blocks of them (rth_decode_path)");
+                "of up to g = min(16, 2048 / head_dim) q heads, or groups in equal blocks of 4 "
+                "to g (rth_decode_path)");
     RTH_REQUIRE(partial != nullptr, "partial must not be null");
     return check_hip(rth::flash_decode_launch(out, q, k_cache, v_cache, k_scale, v_scale,
                                               partial, num_splits, cache_len, num_q_heads,
@@ -468,7 +470,9 @@ int rth_attn_decode_split_paged(uint16_t* out, const uint16_t* q, const uint8_t*
         return rc;
     }
     RTH_REQUIRE(rth::decode_mfma_supported(num_q_heads, num_kv_heads, head_dim),
-                "paged decode supports head_dim 64, 128, 256 with GQA groups of 4-16 q heads or blocks of them (rth_decode_path)");
+                "paged decode supports head_dim 64, 128, 256 with GQA groups of up to g = "
+                "min(16, 2048 / head_dim) q heads, or groups in equal blocks of 4 to g "
+                "(rth_decode_path)");
     RTH_REQUIRE(partial != nullptr, "partial must not be null");
     return check_hip(rth::flash_decode_launch(out, q, k, v, k_scale, v_scale, partial,
                                               num_splits, cache_len, num_q_heads, num_kv_heads,
@@ -495,7 +499,9 @@ int rth_attn_decode_append_split_paged(uint16_t* out, const uint16_t* q, uint8_t
         return rc;
     }
     RTH_REQUIRE(rth::decode_mfma_supported(num_q_heads, num_kv_heads, head_dim),
-                "paged decode supports head_dim 64, 128, 256 with GQA groups of 4-16 q heads or blocks of them (rth_decode_path)");
+                "paged decode supports head_dim 64, 128, 256 with GQA groups of up to g = "
+                "min(16, 2048 / head_dim) q heads, or groups in equal blocks of 4 to g "
+                "(rth_decode_path)");
     RTH_REQUIRE(partial != nullptr, "partial must not be null");
     return check_hip(rth::flash_decode_launch(out, q, k_cache, v_cache, k_scale, v_scale,
                                               partial, num_splits, cache_len, num_q_heads,
