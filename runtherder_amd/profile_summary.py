@@ -6,7 +6,7 @@ markdown, for the text files kept under profiles/.
   python -m runtherder_amd.profile_summary loop <rocprof_dir> <after-substring> <kernel-substring> <count>
 
 "loop": mean tracer durations of the first <count> dispatches matching
-<kernel-substring> that follow the last dispatch matching <after-substring>,
+<kernel-substring> that follow the first dispatch matching <after-substring>,
 and of the dispatch right after each (e.g. a split kernel and its merge).
 """
 from __future__ import annotations
@@ -53,7 +53,7 @@ def loop(root: str, after: str, kernel: str, count: int) -> str:
         rows += list(csv.DictReader(open(f)))
     rows.sort(key=lambda r: int(r["Start_Timestamp"]))
     dur = [int(r["End_Timestamp"]) - int(r["Start_Timestamp"]) for r in rows]
-    start = max((i for i, r in enumerate(rows) if after in r["Kernel_Name"]), default=-1) + 1
+    start = min((i for i, r in enumerate(rows) if after in r["Kernel_Name"]), default=-1) + 1
     first, second, names = [], [], None
     i = start
     while len(first) < count and i + 1 < len(rows):
