@@ -313,6 +313,51 @@ def test_decode_append_fused(cache_len, hq, hkv, d, splits):
     assert mx <= MAX_ABS and mean <= 1e-3, (mx, mean)
 
 
+@pytest.mark.parametrize("d", [64, 128, 256])
+def test_decode_append_fused_special_values(d):
+    """The fused entry's quantizer on rows the append kernel's own tests cover
+    (quantization.cu:224-250): NaN entries (ignored by the amax), +-inf (scale
+    inf, codes from x * 0), an all-zero row (scale 0), bf16 subnormals only,
+    the largest finite bf16 values, mixed with ordinary rows. Cache codes and
+    scales equal the oracle quantizer's bit for bit (head_dim 64 and 128 take
+    the rows loaded at kernel start, 256 the late loads); the output is not
+    checked, as a NaN key makes it NaN by design."""
+    hq, hkv, cache_len, splits = 32, 8, 1000, 64
+    scale = np.float32(1.0 / np.sqrt(d))
+    total = cache_len + 1
+    _, _, k8, v8, ks, vs = make_cache(total, hkv, d, kind="normal", seed=d)
+    kn = O.normal_bf16((hkv, d), 6000 + d)
+    vn = O.normal_bf16((hkv, d), 7000 + d)
+    for x in (kn, vn):
+        x[0, 3], x[0, d - 1] = 0x7FC0, 0xFFC1             # NaNs
+        x[1, 5] = 0x7F80                                  # +inf
+        x[2, :] = 0                                       # zero row
+        x[3, :] = np.arange(1, d + 1, dtype=np.uint16)    # subnormals
+        x[4, ::2] = 0x7F7F                                # +-max finite
+        x[4, 1::2] = 0xFF7F
+        x[5, 7] = 0xFF80                                  # -inf
+    q = O.normal_bf16((hq, d), 8000 + d)
+    rows = slice(cache_len * hkv, total * hkv)
+    kc, vc, ksd, vsd = u8_dev(k8), u8_dev(v8), f32_dev(ks), f32_dev(vs)
+    out = torch.empty((hq, d), dtype=torch.bfloat16, device=DEV)
+    partial = R.new_flash_split_scratch(hq, d, splits)
+    step(f"decode+append special values d={d}")
+    R.flash_decode_append_split_bf16(out, bf16_dev(q), kc, vc, ksd, vsd, bf16_dev(kn),
+                                     bf16_dev(vn), partial, splits, int_dev(cache_len), hq, hkv,
+                                     d, scale)
+    sync()
+    wk, wks = O.quantize_kv_fp8(kn, d)
+    wv, wvs = O.quantize_kv_fp8(vn, d)
+    assert np.array_equal(kc.cpu().numpy()[rows], wk)
+    assert np.array_equal(vc.cpu().numpy()[rows], wv)
+    assert np.array_equal(ksd.cpu().numpy()[rows].view(np.uint32), wks.view(np.uint32))
+    assert np.array_equal(vsd.cpu().numpy()[rows].view(np.uint32), wvs.view(np.uint32))
+    # Rows 6 and 7 are ordinary: their kv heads' outputs stay finite.
+    got = bf16_host(out).astype(np.uint32) << 16
+    finite = np.isfinite(got.view(np.float32))
+    assert finite.reshape(hkv, hq // hkv, d)[6:].all()
+
+
 def test_forced_valu_kernel_matches_oracle():
     """rth_set_decode_kernel(RTH_DECODE_VALU) runs the VALU split kernel for
     a shape the MFMA kernel serves (the A/B switch of the measurements);

@@ -294,3 +294,56 @@ def test_rope_decode_steps_in_a_graph():
         for a, b in zip(gk, ek):
             assert np.array_equal(a.cpu().numpy(), b.cpu().numpy())
         torch.zeros((1 << 20,), device=DEV).sum().item()   # eager work between replays
+
+
+@pytest.mark.parametrize("d", [64, 128, 256])
+def test_decode_steps_special_values(d):
+    """The RoPE and Qwen3 decode steps on extreme rows: k rows of zeros, of
+    bf16 subnormals only, of the largest finite values (their rotation
+    overflows to inf) and of mixed huge and tiny values; v rows with NaN and
+    +-inf entries as well. The cache codes and scales equal the oracle's
+    RMSNorm -> RoPE -> quantizer pipeline bit for bit (the attention output is
+    not checked: an inf or NaN key makes it non-finite by design)."""
+    hq, hkv, cache_len, splits, pos, eps = 32, 8, 500, 32, 777, 1e-6
+    scale = np.float32(1.0 / np.sqrt(d))
+    total = cache_len + 1
+    k8, ks = O.quantize_kv_fp8(O.normal_bf16((total * hkv, d), 9100 + d), d)
+    v8, vs = O.quantize_kv_fp8(O.normal_bf16((total * hkv, d), 9200 + d), d)
+    rows = slice(cache_len * hkv, total * hkv)
+    q = O.normal_bf16((hq, d), 9300 + d)
+    kn = O.normal_bf16((hkv, d), 9400 + d)
+    vn = O.normal_bf16((hkv, d), 9500 + d)
+    for x in (kn, vn):
+        x[0, :] = 0
+        x[1, :] = np.arange(1, d + 1, dtype=np.uint16)
+        x[2, ::2], x[2, 1::2] = 0x7F7F, 0xFF7F
+        x[3, ::3] = 0x7F00
+    vn[4, 3], vn[4, 9], vn[5, 0] = 0x7FC0, 0x7F80, 0xFF80
+    qg = O.normal_bf16((d,), 9600 + d)
+    kg = O.normal_bf16((d,), 9700 + d)
+    inv = inv_table(d, "plain")
+    posd, invd, cl = i32_dev(np.array([pos], np.int32)), f32_dev(inv), int_dev(cache_len)
+    p = np.array([pos], np.int32)
+    lanes = R.rmsnorm_lanes(d)
+    wv, wvs = O.quantize_kv_fp8(vn, d)
+    for norm in (False, True):
+        step(f"decode step special values d={d} norm={norm}")
+        kc, vc, ksd, vsd = u8_dev(k8), u8_dev(v8), f32_dev(ks), f32_dev(vs)
+        out = torch.empty((hq, d), dtype=torch.bfloat16, device=DEV)
+        part = R.new_flash_split_scratch(hq, d, splits)
+        if norm:
+            R.flash_decode_qk_norm_rope_append_split_bf16(
+                out, bf16_dev(q), kc, vc, ksd, vsd, bf16_dev(kn), bf16_dev(vn), bf16_dev(qg),
+                bf16_dev(kg), eps, posd, invd, part, splits, cl, hq, hkv, d, scale)
+            k_t = O.rope_apply_bf16(O.rmsnorm_bf16(kn, kg, eps, lanes)[None], p, inv)[0]
+        else:
+            R.flash_decode_rope_append_split_bf16(out, bf16_dev(q), kc, vc, ksd, vsd,
+                                                  bf16_dev(kn), bf16_dev(vn), posd, invd, part,
+                                                  splits, cl, hq, hkv, d, scale)
+            k_t = O.rope_apply_bf16(kn[None], p, inv)[0]
+        sync()
+        wk, wks = O.quantize_kv_fp8(k_t, d)
+        assert np.array_equal(kc.cpu().numpy()[rows], wk)
+        assert np.array_equal(ksd.cpu().numpy()[rows].view(np.uint32), wks.view(np.uint32))
+        assert np.array_equal(vc.cpu().numpy()[rows], wv)
+        assert np.array_equal(vsd.cpu().numpy()[rows].view(np.uint32), wvs.view(np.uint32))
