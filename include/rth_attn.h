@@ -248,8 +248,9 @@ int rth_attn_decode_rope_append_split_paged(uint16_t* out, const uint16_t* q, ui
  * rmsnorm_bf16_forward(q, q_norm) and (k, k_norm) per head -> rope_bf16 ->
  * KVCache::append -> run (reference src/model/supported/llama/
  * qwen3.cu:189-202), in the two launches of rth_attn_decode_append_split.
- * q and k_new are read only; cache bytes and output are bit-identical to
- * rth_qk_norm_rope_append_fp8 followed by rth_attn_decode_split. Shapes as
+ * q and k_new are read only; the cache row equals rth_qk_norm_rope_append_fp8's
+ * byte for byte, and the output equals rth_attn_decode_append_split on q and
+ * k_new after rth_rmsnorm_bf16 (per head) and rth_rope_bf16. Shapes as
  * rth_attn_decode_rope_append_split. */
 int rth_attn_decode_qk_norm_rope_append_split(
     uint16_t* out, const uint16_t* q, uint8_t* k_cache, uint8_t* v_cache, float* k_scale,

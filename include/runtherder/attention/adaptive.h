@@ -22,6 +22,48 @@ public:
              const int*            cache_len,
              hipStream_t           stream) override;
 
+    // The decode step of one layer as one call of two kernels (no reference
+    // counterpart): KVCache::append of the token k_new, v_new
+    // ([num_kv_heads, head_dim] bf16) at row *cache_len, then
+    // run(out, q, kv, 1, cache_len) (reference llama3.cu:232-234). kv must view
+    // writable slabs (KVCache::view / PagedKVCache views); paged when
+    // kv.block_table is set. Bit-identical to append followed by run.
+    void run_decode_append(__hip_bfloat16*       out,
+                           const __hip_bfloat16* q,
+                           const KVView&         kv,
+                           const __hip_bfloat16* k_new,
+                           const __hip_bfloat16* v_new,
+                           const int*            cache_len,
+                           hipStream_t           stream);
+
+    // The same step with rope_bf16(q, k_new) (positions[0], inv_freq;
+    // reference rope.cu:14-55) applied in the split kernel's registers
+    // (llama3.cu:228-234 in two launches). q and k_new are read only.
+    void run_decode_rope_append(__hip_bfloat16*       out,
+                                const __hip_bfloat16* q,
+                                const KVView&         kv,
+                                const __hip_bfloat16* k_new,
+                                const __hip_bfloat16* v_new,
+                                const int*            positions,
+                                const float*          inv_freq,
+                                const int*            cache_len,
+                                hipStream_t           stream);
+
+    // Qwen3's order (qwen3.cu:189-202): per-head RMSNorm of q and k_new with
+    // the q_norm / k_norm gains ([head_dim] bf16), RoPE, append, decode.
+    void run_decode_qk_norm_rope_append(__hip_bfloat16*       out,
+                                        const __hip_bfloat16* q,
+                                        const KVView&         kv,
+                                        const __hip_bfloat16* k_new,
+                                        const __hip_bfloat16* v_new,
+                                        const __hip_bfloat16* q_norm,
+                                        const __hip_bfloat16* k_norm,
+                                        float                 eps,
+                                        const int*            positions,
+                                        const float*          inv_freq,
+                                        const int*            cache_len,
+                                        hipStream_t           stream);
+
     [[nodiscard]] int num_splits() const noexcept { return num_splits_; }
 
 private:

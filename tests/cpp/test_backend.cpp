@@ -13,8 +13,10 @@
 #include <memory>
 #include <vector>
 
+#include <runtherder/attention/adaptive.h>
 #include <runtherder/attention/factory.h>
 #include <runtherder/engine/kv_cache.h>
+#include <runtherder/kernels/rmsnorm.h>
 #include <runtherder/kernels/rope.h>
 
 #include "rth_oracle.h"
@@ -232,6 +234,121 @@ int run_rope_case() {
     return (same_two && same_ref) ? 0 : 1;
 }
 
+// AdaptiveAttention's decode-step methods against the caller sequences they
+// replace, on two caches holding the same 40-token prefix, for three steps
+// each: run_decode_append vs append -> run; run_decode_rope_append vs
+// rope_bf16 -> append -> run (llama3.cu:228-234); run_decode_qk_norm_rope_append
+// vs rmsnorm_bf16_forward (q, k per head) -> rope_bf16 -> append -> run
+// (qwen3.cu:189-202). Cache bytes must be identical; the outputs agree within
+// the attention tolerance (the fused step folds the appended key in after the
+// cache's keys, a different summation order).
+int run_decode_step_case() {
+    const int   Hq = 24, Hkv = 8, D = 128, S = 64, pre = 40, steps = 3;
+    const float scale = 1.0f / std::sqrt(static_cast<float>(D)), eps = 1e-6f;
+    runtherder::attention::AdaptiveAttention backend(AttnConfig{Hq, Hkv, D, scale});
+    std::vector<uint16_t> kh(static_cast<size_t>(pre + steps) * Hkv * D), vh(kh.size()),
+        qh(static_cast<size_t>(steps) * Hq * D), gq(D), gk(D);
+    rth_ref_fill_normal_bf16(kh.data(), static_cast<int64_t>(kh.size()), 1100);
+    rth_ref_fill_normal_bf16(vh.data(), static_cast<int64_t>(vh.size()), 1101);
+    rth_ref_fill_normal_bf16(qh.data(), static_cast<int64_t>(qh.size()), 1102);
+    rth_ref_fill_normal_bf16(gq.data(), D, 1103);
+    rth_ref_fill_normal_bf16(gk.data(), D, 1104);
+    std::vector<float> inv(D / 2);
+    rth_ref_rope_inv_freq_plain(inv.data(), D, 1e6f);
+
+    auto* dk   = dev_alloc<uint16_t>(kh.size());
+    auto* dv   = dev_alloc<uint16_t>(vh.size());
+    auto* dq   = dev_alloc<uint16_t>(qh.size());
+    auto* dq2  = dev_alloc<uint16_t>(static_cast<size_t>(Hq) * D);
+    auto* dk2  = dev_alloc<uint16_t>(static_cast<size_t>(Hkv) * D);
+    auto* dgq  = dev_alloc<uint16_t>(D);
+    auto* dgk  = dev_alloc<uint16_t>(D);
+    auto* dinv = dev_alloc<float>(inv.size());
+    auto* o1   = dev_alloc<uint16_t>(static_cast<size_t>(Hq) * D);
+    auto* o2   = dev_alloc<uint16_t>(static_cast<size_t>(Hq) * D);
+    int*  pos  = dev_alloc<int>(1);
+    RUNTHERDER_HIP_CHECK(hipMemcpy(dk, kh.data(), kh.size() * 2, hipMemcpyHostToDevice));
+    RUNTHERDER_HIP_CHECK(hipMemcpy(dv, vh.data(), vh.size() * 2, hipMemcpyHostToDevice));
+    RUNTHERDER_HIP_CHECK(hipMemcpy(dq, qh.data(), qh.size() * 2, hipMemcpyHostToDevice));
+    RUNTHERDER_HIP_CHECK(hipMemcpy(dgq, gq.data(), D * 2, hipMemcpyHostToDevice));
+    RUNTHERDER_HIP_CHECK(hipMemcpy(dgk, gk.data(), D * 2, hipMemcpyHostToDevice));
+    RUNTHERDER_HIP_CHECK(hipMemcpy(dinv, inv.data(), inv.size() * 4, hipMemcpyHostToDevice));
+    auto bf = [](uint16_t* p) { return reinterpret_cast<__hip_bfloat16*>(p); };
+    auto cbf = [](const uint16_t* p) { return reinterpret_cast<const __hip_bfloat16*>(p); };
+    const char* names[3] = {"decode_append", "decode_rope_append", "decode_qk_norm_rope_append"};
+
+    int fails = 0;
+    for (int mode = 0; mode < 3; ++mode) {
+        KVCache a(1, S, Hkv, D), b(1, S, Hkv, D);
+        const int zero = 0;
+        RUNTHERDER_HIP_CHECK(hipMemcpy(pos, &zero, sizeof(int), hipMemcpyHostToDevice));
+        a.append(0, cbf(dk), cbf(dv), pre, pos, nullptr);
+        b.append(0, cbf(dk), cbf(dv), pre, pos, nullptr);
+        for (int s = 0; s < steps; ++s) {
+            const int p = pre + s;
+            RUNTHERDER_HIP_CHECK(hipMemcpy(pos, &p, sizeof(int), hipMemcpyHostToDevice));
+            const uint16_t* q  = dq + static_cast<size_t>(s) * Hq * D;
+            const uint16_t* kn = dk + static_cast<size_t>(p) * Hkv * D;
+            const uint16_t* vn = dv + static_cast<size_t>(p) * Hkv * D;
+            if (mode == 0) {
+                backend.run_decode_append(bf(o1), cbf(q), a.view(0), cbf(kn), cbf(vn), pos,
+                                          nullptr);
+                b.append(0, cbf(kn), cbf(vn), 1, pos, nullptr);
+                backend.run(bf(o2), cbf(q), b.view(0), 1, pos, nullptr);
+            } else {
+                RUNTHERDER_HIP_CHECK(hipMemcpy(dq2, q, Hq * D * 2, hipMemcpyDeviceToDevice));
+                RUNTHERDER_HIP_CHECK(hipMemcpy(dk2, kn, Hkv * D * 2, hipMemcpyDeviceToDevice));
+                if (mode == 1) {
+                    backend.run_decode_rope_append(bf(o1), cbf(q), a.view(0), cbf(kn), cbf(vn),
+                                                   pos, dinv, pos, nullptr);
+                } else {
+                    backend.run_decode_qk_norm_rope_append(bf(o1), cbf(q), a.view(0), cbf(kn),
+                                                           cbf(vn), cbf(dgq), cbf(dgk), eps, pos,
+                                                           dinv, pos, nullptr);
+                    runtherder::kernels::rmsnorm_bf16_forward(bf(dq2), cbf(dq2), cbf(dgq), Hq, D,
+                                                              eps, nullptr);
+                    runtherder::kernels::rmsnorm_bf16_forward(bf(dk2), cbf(dk2), cbf(dgk), Hkv,
+                                                              D, eps, nullptr);
+                }
+                runtherder::kernels::rope_bf16(bf(dq2), bf(dk2), pos, dinv, 1, Hq, Hkv, D,
+                                               nullptr);
+                b.append(0, cbf(dk2), cbf(vn), 1, pos, nullptr);
+                backend.run(bf(o2), cbf(dq2), b.view(0), 1, pos, nullptr);
+            }
+            RUNTHERDER_HIP_CHECK(hipDeviceSynchronize());
+            std::vector<uint16_t> g1(static_cast<size_t>(Hq) * D), g2(g1.size());
+            RUNTHERDER_HIP_CHECK(hipMemcpy(g1.data(), o1, g1.size() * 2, hipMemcpyDeviceToHost));
+            RUNTHERDER_HIP_CHECK(hipMemcpy(g2.data(), o2, g2.size() * 2, hipMemcpyDeviceToHost));
+            const size_t         n8 = static_cast<size_t>(p + 1) * Hkv * D, ns = n8 / D;
+            std::vector<uint8_t> ka(n8), kb(n8), va(n8), vb(n8);
+            std::vector<float>   ksa(ns), ksb(ns);
+            const auto           av = a.view(0), bv = b.view(0);
+            RUNTHERDER_HIP_CHECK(hipMemcpy(ka.data(), av.k, n8, hipMemcpyDeviceToHost));
+            RUNTHERDER_HIP_CHECK(hipMemcpy(kb.data(), bv.k, n8, hipMemcpyDeviceToHost));
+            RUNTHERDER_HIP_CHECK(hipMemcpy(va.data(), av.v, n8, hipMemcpyDeviceToHost));
+            RUNTHERDER_HIP_CHECK(hipMemcpy(vb.data(), bv.v, n8, hipMemcpyDeviceToHost));
+            RUNTHERDER_HIP_CHECK(hipMemcpy(ksa.data(), av.k_scale, ns * 4, hipMemcpyDeviceToHost));
+            RUNTHERDER_HIP_CHECK(hipMemcpy(ksb.data(), bv.k_scale, ns * 4, hipMemcpyDeviceToHost));
+            const bool  bytes_ok = ka == kb && va == vb &&
+                                  std::memcmp(ksa.data(), ksb.data(), ns * 4) == 0;
+            const Stats st = compare(g1, g2);
+            const bool  ok = bytes_ok && st.max_abs <= 2e-2 && st.mean_abs <= 1e-3;
+            std::printf("%s step=%d pos=%d bytes_identical=%d max_abs=%.3e mean_abs=%.3e %s\n",
+                        names[mode], s, p, bytes_ok ? 1 : 0, st.max_abs, st.mean_abs,
+                        ok ? "OK" : "FAIL");
+            std::fflush(stdout);
+            fails += ok ? 0 : 1;
+        }
+    }
+    for (void* ptr : {static_cast<void*>(dk), static_cast<void*>(dv), static_cast<void*>(dq),
+                      static_cast<void*>(dq2), static_cast<void*>(dk2), static_cast<void*>(dgq),
+                      static_cast<void*>(dgk), static_cast<void*>(dinv), static_cast<void*>(o1),
+                      static_cast<void*>(o2), static_cast<void*>(pos)}) {
+        (void)hipFree(ptr);
+    }
+    return fails;
+}
+
 }  // namespace
 
 int main() {
@@ -239,6 +356,7 @@ int main() {
     fails += run_case(BackendKind::Adaptive, "adaptive");
     fails += run_case(BackendKind::Naive, "naive");
     fails += run_rope_case();
+    fails += run_decode_step_case();
     std::printf("%s\n", fails == 0 ? "ALL OK" : "FAILURES");
     return fails == 0 ? 0 : 1;
 }
