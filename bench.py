@@ -120,7 +120,7 @@ def bench_decode(torch, R, args, stream):
         for s in range(n_steps):
             for l in range(L):
                 if fused:
-                    backend.run_decode_append(out[s, l], qs[s, l], cache.view(l), ks[s, l],
+                    backend.run_decode_append(out[s, l], qs[s, l], cache.slabs(l), ks[s, l],
                                               vs[s, l], pos)
                 else:
                     cache.append(l, ks[s, l], vs[s, l], 1, pos)
@@ -205,7 +205,7 @@ def bench_decode(torch, R, args, stream):
     def run_rope_steps(mode, n_steps):
         for s in range(n_steps):
             for l in range(L):
-                q, k, v, o, view = qs_r[s, l], ks_r[s, l], vs[s, l], out[s, l], cache.view(l)
+                q, k, v, o, view = qs_r[s, l], ks_r[s, l], vs[s, l], out[s, l], cache.slabs(l)
                 if mode == "fused":
                     backend.run_decode_rope_append(o, q, view, k, v, pos, inv, pos)
                 elif mode == "rope+fused":
@@ -465,6 +465,26 @@ def profile_traffic(name="decode_attn_8k_pmc_traffic.md"):
     return None
 
 
+def host_cores():
+    """Threads for the CPU baselines: every core this process may run on (the
+    affinity mask), capped by a cgroup CPU quota when one is set; plus the
+    machine's CPU count (nproc) for the record."""
+    nproc = os.cpu_count() or 1
+    try:
+        usable = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        usable = nproc
+    quota = None
+    try:
+        q, period = Path("/sys/fs/cgroup/cpu.max").read_text().split()[:2]
+        if q != "max":
+            quota = max(1, int(int(q) // int(period)))
+    except (OSError, ValueError):
+        pass
+    cores = min(usable, quota) if quota else usable
+    return max(1, cores), nproc, quota
+
+
 def cpu_baseline(torch, dec, budget_s=10.0):
     """The oracle (C restatement of the reference's naive fp32 attention,
     reference src/kernels/attention.cu:34-91) on host threads: the same decode
@@ -474,8 +494,10 @@ def cpu_baseline(torch, dec, budget_s=10.0):
     import numpy as np
     import oracle_lib as O
 
-    cores = max(1, min(16, os.cpu_count() or 1))
+    usable, nproc, quota = host_cores()
     hq, hkv, d, depth = dec["hq"], dec["hkv"], dec["d"], dec["depth"]
+    # the oracle runs one thread per (token, q head) row at most, 256 at most
+    cores = min(usable, hq, 256)
     cache = dec["cache"]
     keys = depth + 1
     host = []
@@ -495,7 +517,7 @@ def cpu_baseline(torch, dec, budget_s=10.0):
         calls += 1
     nbytes = calls * decode_bytes(keys, hq, hkv, d)
     return {"value": round(nbytes / t_total / 1e9, 3), "unit": "GB/s", "cores": cores,
-            "kind": "port",
+            "usable_cores": usable, "nproc": nproc, "cgroup_cpu_quota": quota, "kind": "port",
             "sample": f"{calls} decode calls (cycling the 28 layers) at ctx {keys}, 24Q/8KV, "
                       f"fp32 two-pass naive attention over the same FP8 cache bytes and queries, "
                       f"{t_total:.1f} s on {cores} threads"}
@@ -511,8 +533,9 @@ def cpu_prefill_baseline(budget_s=6.0):
     import numpy as np
     import oracle_lib as O
 
-    cores = max(1, min(16, os.cpu_count() or 1))
+    usable, nproc, quota = host_cores()
     n, hq, hkv, d = 1021, 24, 8, 128
+    cores = min(usable, n * hq, 256)
     q = O.normal_bf16((n, hq, d), 71)
     k8, ks = O.quantize_kv_fp8(O.normal_bf16((n * hkv, d), 72), d)
     v8, vs = O.quantize_kv_fp8(O.normal_bf16((n * hkv, d), 73), d)
@@ -525,7 +548,7 @@ def cpu_prefill_baseline(budget_s=6.0):
         calls += 1
     fl = calls * prefill_flops(n, 0, hq, d)
     return {"value": round(fl / t_total / 1e9, 2), "unit": "GFLOP/s", "cores": cores,
-            "kind": "port", "ms_per_call": round(1e3 * t_total / calls, 1),
+            "usable_cores": usable, "nproc": nproc, "cgroup_cpu_quota": quota, "kind": "port", "ms_per_call": round(1e3 * t_total / calls, 1),
             "sample": f"{calls} calls of config 2 (n=1021, 24Q/8KV, causal, clen 0), fp32 "
                       f"two-pass naive attention over the FP8 cache, {t_total:.1f} s on "
                       f"{cores} threads"}
@@ -625,7 +648,7 @@ def main() -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "e4m3-kv/decode-bf16-mfma/prefill-fp8(qk,exact-q-split)+f16(pv)-mfma/fp32-acc",
+        "dtype": "e4m3-kv/decode-bf16-mfma/prefill-fp8(qk,two-part-e4m3-q-split:exact>=2^-14-of-row-max)+f16(pv)-mfma/fp32-acc",
         "data": "synthetic: N(0,1) bf16 q/k/v, k/v quantized to FP8 E4M3 by the append kernel",
         "config": {
             "workload": "config3: 28-layer Llama-3.2-3B-shaped decode attention, 24Q/8KV, "

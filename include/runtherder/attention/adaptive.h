@@ -25,12 +25,12 @@ public:
     // The decode step of one layer as one call of two kernels (no reference
     // counterpart): KVCache::append of the token k_new, v_new
     // ([num_kv_heads, head_dim] bf16) at row *cache_len, then
-    // run(out, q, kv, 1, cache_len) (reference llama3.cu:232-234). kv must view
-    // writable slabs (KVCache::view / PagedKVCache views); paged when
-    // kv.block_table is set. Bit-identical to append followed by run.
+    // run(out, q, kv.view(), 1, cache_len) (reference llama3.cu:232-234). kv
+    // holds the layer's writable slabs (KVCache::slabs / PagedKVCache::slabs);
+    // paged when kv.block_table is set. Bit-identical to append followed by run.
     void run_decode_append(__hip_bfloat16*       out,
                            const __hip_bfloat16* q,
-                           const KVView&         kv,
+                           const KVSlabs&        kv,
                            const __hip_bfloat16* k_new,
                            const __hip_bfloat16* v_new,
                            const int*            cache_len,
@@ -41,7 +41,7 @@ public:
     // (llama3.cu:228-234 in two launches). q and k_new are read only.
     void run_decode_rope_append(__hip_bfloat16*       out,
                                 const __hip_bfloat16* q,
-                                const KVView&         kv,
+                                const KVSlabs&        kv,
                                 const __hip_bfloat16* k_new,
                                 const __hip_bfloat16* v_new,
                                 const int*            positions,
@@ -53,7 +53,7 @@ public:
     // the q_norm / k_norm gains ([head_dim] bf16), RoPE, append, decode.
     void run_decode_qk_norm_rope_append(__hip_bfloat16*       out,
                                         const __hip_bfloat16* q,
-                                        const KVView&         kv,
+                                        const KVSlabs&        kv,
                                         const __hip_bfloat16* k_new,
                                         const __hip_bfloat16* v_new,
                                         const __hip_bfloat16* q_norm,

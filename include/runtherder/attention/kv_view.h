@@ -21,4 +21,22 @@ struct KVView {
     int        block_size  = 0;
 };
 
+// The writable slabs of one layer, for the fused decode steps that store the
+// new token into the cache (no reference counterpart: the reference appends
+// through KVCache::append and only ever reads through KVView). Same layout
+// and paged fields as KVView; KVCache::slabs / PagedKVCache::slabs build it.
+struct KVSlabs {
+    __hip_fp8_e4m3* k;
+    __hip_fp8_e4m3* v;
+    float*          k_scale;
+    float*          v_scale;
+    const int*      block_table = nullptr;
+    int             block_size  = 0;
+
+    // The read-only view of the same slabs (for AttentionBackend::run).
+    [[nodiscard]] KVView view() const noexcept {
+        return KVView{k, v, k_scale, v_scale, block_table, block_size};
+    }
+};
+
 }  // namespace runtherder::attention

@@ -118,6 +118,16 @@ public:
                                  v_scale_.get() + sbase};
     }
 
+    // The writable slabs of `layer`, for AdaptiveAttention's fused decode
+    // steps (which store the new token into them).
+    [[nodiscard]] attention::KVSlabs slabs(int layer) {
+        RUNTHERDER_CHECK(layer >= 0 && layer < num_layers_, "KVCache slabs layer out of range");
+        const std::size_t base  = static_cast<std::size_t>(layer) * layer_stride_;
+        const std::size_t sbase = static_cast<std::size_t>(layer) * scale_layer_stride_;
+        return attention::KVSlabs{k_.get() + base, v_.get() + base, k_scale_.get() + sbase,
+                                  v_scale_.get() + sbase};
+    }
+
     [[nodiscard]] int max_seq_len() const noexcept { return max_seq_len_; }
 
 private:

@@ -64,6 +64,14 @@ public:
                                  v_scale_.get() + sbase, block_table, block_size_};
     }
 
+    [[nodiscard]] attention::KVSlabs slabs(int layer, const int* block_table) {
+        RUNTHERDER_CHECK(layer >= 0 && layer < num_layers_, "KVCache slabs layer out of range");
+        const std::size_t base  = static_cast<std::size_t>(layer) * layer_stride_;
+        const std::size_t sbase = static_cast<std::size_t>(layer) * scale_layer_stride_;
+        return attention::KVSlabs{k_.get() + base, v_.get() + base, k_scale_.get() + sbase,
+                                  v_scale_.get() + sbase, block_table, block_size_};
+    }
+
     [[nodiscard]] int block_size() const noexcept { return block_size_; }
     [[nodiscard]] int num_blocks() const noexcept { return num_blocks_; }
 

@@ -14,11 +14,15 @@
 
 namespace runtherder::kernels {
 
-// Floats of decode scratch for max_splits splits: [Hq, S] m, then l, then
-// [Hq, S, D] acc, one contiguous slab (same formula as the reference).
-[[nodiscard]] inline std::size_t flash_split_scratch_floats(int num_q_heads, int head_dim,
-                                                            int max_splits) {
-    return rth_split_scratch_floats(num_q_heads, head_dim, max_splits);
+// Floats of decode scratch for max_splits splits: Hq*S m, then Hq*S l, then
+// Hq*S*D acc values, one contiguous slab (same formula as the reference, and as
+// rth_split_scratch_floats; usable in constant expressions as the reference's).
+[[nodiscard]] constexpr std::size_t flash_split_scratch_floats(int num_q_heads, int head_dim,
+                                                               int max_splits) {
+    const std::size_t heads  = static_cast<std::size_t>(num_q_heads);
+    const std::size_t splits = static_cast<std::size_t>(max_splits);
+    const std::size_t dim    = static_cast<std::size_t>(head_dim);
+    return heads * splits * 2 + heads * splits * dim;
 }
 
 // One query token attends *cache_len + 1 keys in num_splits key ranges merged by

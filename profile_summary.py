@@ -1,9 +1,9 @@
 """Summaries of rocprofv3 output (kernel-trace stats and --pmc counters) as
 markdown, for the text files kept under profiles/.
 
-  python -m runtherder_amd.profile_summary stats <rocprof_dir>
-  python -m runtherder_amd.profile_summary pmc <rocprof_dir> [kernel-substring]
-  python -m runtherder_amd.profile_summary loop <rocprof_dir> <after-substring> <kernel-substring> <count>
+  python profile_summary.py stats <rocprof_dir>
+  python profile_summary.py pmc <rocprof_dir> [kernel-substring]
+  python profile_summary.py loop <rocprof_dir> <after-substring> <kernel-substring> <count>
 
 "loop": mean tracer durations of the first <count> dispatches matching
 <kernel-substring> that follow the first dispatch matching <after-substring>,

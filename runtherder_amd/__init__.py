@@ -13,6 +13,7 @@ from .ops import (  # noqa: F401
     AttnConfig,
     BackendKind,
     KVCache,
+    KVSlabs,
     KVView,
     NaiveAttention,
     PagedKVCache,

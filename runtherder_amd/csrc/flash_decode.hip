@@ -1051,24 +1051,20 @@ __device__ __forceinline__ void decode_body(
             part_l[slot]       = L;
         }
     } else {
-        // O^T goes through this wave's LDS rows so the stores run along d.
-        float* so = sm_o[wave];
+        // Straight from the MFMA layout: lane (n, g) holds, for each r, the
+        // kOMfma consecutive values d = kVBytes * (4g + r) + c of q head n
+        // (oacc[c][r]), so it stores them as 16-byte runs with no LDS pass.
         if (n < G) {
+            const int64_t slot = static_cast<int64_t>(kvh * G + n) * num_splits + si;
+            float*        po   = part_o + slot * D;
 #pragma unroll
-            for (int c = 0; c < T::kOMfma; ++c) {
+            for (int r = 0; r < 4; ++r) {
 #pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    so[n * D + T::kVBytes * (4 * g + r) + c] = oacc[c][r];
+                for (int c = 0; c < T::kOMfma; c += 4) {
+                    *reinterpret_cast<f32x4*>(po + T::kVBytes * (4 * g + r) + c) =
+                        f32x4{oacc[c][r], oacc[c + 1][r], oacc[c + 2][r], oacc[c + 3][r]};
                 }
             }
-        }
-        __builtin_amdgcn_wave_barrier();
-        for (int e = lane; e < G * (D / 4); e += kWave) {
-            const int     h    = e / (D / 4);
-            const int     d0   = 4 * (e - h * (D / 4));
-            const int64_t slot = static_cast<int64_t>(kvh * G + h) * num_splits + si;
-            *reinterpret_cast<f32x4*>(&part_o[slot * D + d0]) =
-                *reinterpret_cast<const f32x4*>(&so[h * D + d0]);
         }
         if (g == 0 && n < G) {
             const int64_t slot = static_cast<int64_t>(kvh * G + n) * num_splits + si;

@@ -19,12 +19,15 @@
 //    XOR-swizzled by row so the operand reads are bank-conflict free), ahead
 //    of use, with no registers or VALU work.
 //  * Scores S^T = K Q^T run on the fp8 MFMA v_mfma_scale_f32_32x32x64_f8f6f4
-//    with A = the raw K codes from LDS and B = Q split exactly into two E4M3
+//    with A = the raw K codes from LDS and B = Q split into two E4M3
 //    parts: q * 2^a = hi + lo / 16 (a per row, so the row maximum lands in
 //    [128, 256)), the MFMA's per-lane E8M0 scales undoing 2^a and 16. A bf16
-//    q has 8 significant bits and hi takes the top 4, so the split is exact
-//    and every product is the exact code * q product, accumulated in fp32 -
-//    the same scores as exact E4M3 codes times bf16 q.
+//    q has 8 significant bits and hi takes the top 4, so for scaled elements
+//    |y| >= 2^-6 the split is exact and every product is the exact code * q
+//    product, accumulated in fp32. Below 2^-6 (elements more than ~13
+//    binades under their row maximum) lo falls into E4M3 subnormals and the
+//    split errs by at most 2^-14 in scaled units, 2^-21 of the row maximum
+//    (tests/test_prefill_q_split.py checks both over every bf16 value).
 //  * Each lane owns one query row (the S^T column), so the softmax needs no
 //    cross-lane step except on a rebase. t = s * (k_scale * scale * log2 e)
 //    - m_ref against a lazy reference maximum; p = 2^t rounded to f16, the

@@ -68,20 +68,7 @@ void AdaptiveAttention::run(__hip_bfloat16* out, const __hip_bfloat16* q, const 
 
 namespace {
 
-// The slabs a decode step writes its token into: a KVView holds them as const
-// (run only reads), but the view of a KVCache points at its writable memory.
-struct Slabs {
-    std::uint8_t* k;
-    std::uint8_t* v;
-    float*        ks;
-    float*        vs;
-};
-
-Slabs writable(const KVView& kv) {
-    return {reinterpret_cast<std::uint8_t*>(const_cast<__hip_fp8_e4m3*>(kv.k)),
-            reinterpret_cast<std::uint8_t*>(const_cast<__hip_fp8_e4m3*>(kv.v)),
-            const_cast<float*>(kv.k_scale), const_cast<float*>(kv.v_scale)};
-}
+std::uint8_t* u8(__hip_fp8_e4m3* p) { return reinterpret_cast<std::uint8_t*>(p); }
 
 const std::uint16_t* u16(const __hip_bfloat16* p) {
     return reinterpret_cast<const std::uint16_t*>(p);
@@ -90,61 +77,58 @@ const std::uint16_t* u16(const __hip_bfloat16* p) {
 }  // namespace
 
 void AdaptiveAttention::run_decode_append(__hip_bfloat16* out, const __hip_bfloat16* q,
-                                          const KVView& kv, const __hip_bfloat16* k_new,
+                                          const KVSlabs& kv, const __hip_bfloat16* k_new,
                                           const __hip_bfloat16* v_new, const int* cache_len,
                                           hipStream_t stream) {
-    const Slabs s = writable(kv);
     auto*       o = reinterpret_cast<std::uint16_t*>(out);
     if (kv.block_table != nullptr) {
         RUNTHERDER_RTH_CHECK(rth_attn_decode_append_split_paged(
-            o, u16(q), s.k, s.v, s.ks, s.vs, kv.block_table, kv.block_size, u16(k_new),
+            o, u16(q), u8(kv.k), u8(kv.v), kv.k_scale, kv.v_scale, kv.block_table, kv.block_size, u16(k_new),
             u16(v_new), partial_.get(), num_splits_, cache_len, config_.num_q_heads,
             config_.num_kv_heads, config_.head_dim, config_.scale, stream));
         return;
     }
     RUNTHERDER_RTH_CHECK(rth_attn_decode_append_split(
-        o, u16(q), s.k, s.v, s.ks, s.vs, u16(k_new), u16(v_new), partial_.get(), num_splits_,
+        o, u16(q), u8(kv.k), u8(kv.v), kv.k_scale, kv.v_scale, u16(k_new), u16(v_new), partial_.get(), num_splits_,
         cache_len, config_.num_q_heads, config_.num_kv_heads, config_.head_dim, config_.scale,
         stream));
 }
 
 void AdaptiveAttention::run_decode_rope_append(__hip_bfloat16* out, const __hip_bfloat16* q,
-                                               const KVView& kv, const __hip_bfloat16* k_new,
+                                               const KVSlabs& kv, const __hip_bfloat16* k_new,
                                                const __hip_bfloat16* v_new, const int* positions,
                                                const float* inv_freq, const int* cache_len,
                                                hipStream_t stream) {
-    const Slabs s = writable(kv);
     auto*       o = reinterpret_cast<std::uint16_t*>(out);
     if (kv.block_table != nullptr) {
         RUNTHERDER_RTH_CHECK(rth_attn_decode_rope_append_split_paged(
-            o, u16(q), s.k, s.v, s.ks, s.vs, kv.block_table, kv.block_size, u16(k_new),
+            o, u16(q), u8(kv.k), u8(kv.v), kv.k_scale, kv.v_scale, kv.block_table, kv.block_size, u16(k_new),
             u16(v_new), positions, inv_freq, partial_.get(), num_splits_, cache_len,
             config_.num_q_heads, config_.num_kv_heads, config_.head_dim, config_.scale, stream));
         return;
     }
     RUNTHERDER_RTH_CHECK(rth_attn_decode_rope_append_split(
-        o, u16(q), s.k, s.v, s.ks, s.vs, u16(k_new), u16(v_new), positions, inv_freq,
+        o, u16(q), u8(kv.k), u8(kv.v), kv.k_scale, kv.v_scale, u16(k_new), u16(v_new), positions, inv_freq,
         partial_.get(), num_splits_, cache_len, config_.num_q_heads, config_.num_kv_heads,
         config_.head_dim, config_.scale, stream));
 }
 
 void AdaptiveAttention::run_decode_qk_norm_rope_append(
-    __hip_bfloat16* out, const __hip_bfloat16* q, const KVView& kv, const __hip_bfloat16* k_new,
+    __hip_bfloat16* out, const __hip_bfloat16* q, const KVSlabs& kv, const __hip_bfloat16* k_new,
     const __hip_bfloat16* v_new, const __hip_bfloat16* q_norm, const __hip_bfloat16* k_norm,
     float eps, const int* positions, const float* inv_freq, const int* cache_len,
     hipStream_t stream) {
-    const Slabs s = writable(kv);
     auto*       o = reinterpret_cast<std::uint16_t*>(out);
     if (kv.block_table != nullptr) {
         RUNTHERDER_RTH_CHECK(rth_attn_decode_qk_norm_rope_append_split_paged(
-            o, u16(q), s.k, s.v, s.ks, s.vs, kv.block_table, kv.block_size, u16(k_new),
+            o, u16(q), u8(kv.k), u8(kv.v), kv.k_scale, kv.v_scale, kv.block_table, kv.block_size, u16(k_new),
             u16(v_new), u16(q_norm), u16(k_norm), eps, positions, inv_freq, partial_.get(),
             num_splits_, cache_len, config_.num_q_heads, config_.num_kv_heads, config_.head_dim,
             config_.scale, stream));
         return;
     }
     RUNTHERDER_RTH_CHECK(rth_attn_decode_qk_norm_rope_append_split(
-        o, u16(q), s.k, s.v, s.ks, s.vs, u16(k_new), u16(v_new), u16(q_norm), u16(k_norm), eps,
+        o, u16(q), u8(kv.k), u8(kv.v), kv.k_scale, kv.v_scale, u16(k_new), u16(v_new), u16(q_norm), u16(k_norm), eps,
         positions, inv_freq, partial_.get(), num_splits_, cache_len, config_.num_q_heads,
         config_.num_kv_heads, config_.head_dim, config_.scale, stream));
 }

@@ -288,6 +288,24 @@ class KVView:
     block_size: int = 0
 
 
+@dataclass(frozen=True)
+class KVSlabs(KVView):
+    """The writable slabs of one layer (KVCache.slabs / PagedKVCache.slabs),
+    for the fused decode steps that store the new token into the cache. No
+    reference counterpart: the reference appends through KVCache::append and
+    reads through KVView only."""
+
+    def view(self) -> KVView:
+        return KVView(self.k, self.v, self.k_scale, self.v_scale, self.block_table,
+                      self.block_size)
+
+
+def _need_slabs(kv):
+    if not isinstance(kv, KVSlabs):
+        raise TypeError("the fused decode steps write the cache: pass KVCache.slabs(layer) "
+                        "(or PagedKVCache.slabs(layer, block_table)), not a read-only view")
+
+
 class KVCache:
     """reference include/runtherder/engine/kv_cache.h:23-104"""
 
@@ -343,6 +361,11 @@ class KVCache:
             raise ValueError("KVCache view layer out of range")
         return KVView(self.k[layer], self.v[layer], self.k_scale[layer], self.v_scale[layer])
 
+    def slabs(self, layer) -> KVSlabs:
+        if not 0 <= layer < self.num_layers:
+            raise ValueError("KVCache slabs layer out of range")
+        return KVSlabs(self.k[layer], self.v[layer], self.k_scale[layer], self.v_scale[layer])
+
     def max_seq_len(self) -> int:
         return self._max_seq_len
 
@@ -382,6 +405,13 @@ class PagedKVCache:
         _need(block_table, torch.int32, "block_table")
         return KVView(self.k[layer], self.v[layer], self.k_scale[layer], self.v_scale[layer],
                       block_table, self.block_size)
+
+    def slabs(self, layer, block_table) -> KVSlabs:
+        if not 0 <= layer < self.num_layers:
+            raise ValueError("KVCache slabs layer out of range")
+        _need(block_table, torch.int32, "block_table")
+        return KVSlabs(self.k[layer], self.v[layer], self.k_scale[layer], self.v_scale[layer],
+                       block_table, self.block_size)
 
 
 class AttentionBackend:
@@ -427,7 +457,8 @@ class AdaptiveAttention(AttentionBackend):
 
     def run_decode_append(self, out, q, kv, k_new, v_new, cache_len, stream=None):
         """KVCache.append(layer, k_new, v_new, 1, cache_len) + run(..., n_new=1)
-        in one call (the view's slabs receive the new token)."""
+        in one call; kv is the layer's KVSlabs (they receive the new token)."""
+        _need_slabs(kv)
         c = self.config
         if kv.block_table is not None:
             _ffi.call("rth_attn_decode_append_split_paged", _p(out), _p(q), _p(kv.k), _p(kv.v),
@@ -446,6 +477,7 @@ class AdaptiveAttention(AttentionBackend):
         """rope_bf16(q, k_new, positions, inv_freq) + KVCache.append(layer, k_new,
         v_new, 1, cache_len) + run(..., n_new=1) in one call; q and k_new are
         read only (the rotation happens in registers)."""
+        _need_slabs(kv)
         c = self.config
         if kv.block_table is not None:
             _ffi.call("rth_attn_decode_rope_append_split_paged", _p(out), _p(q), _p(kv.k),
@@ -464,6 +496,7 @@ class AdaptiveAttention(AttentionBackend):
                                        positions, inv_freq, cache_len, stream=None):
         """Qwen3 order: per-head RMSNorm(q, q_norm) and (k_new, k_norm), RoPE,
         KVCache.append and run(..., n_new=1) in one call; q and k_new read only."""
+        _need_slabs(kv)
         c = self.config
         if kv.block_table is not None:
             _ffi.call("rth_attn_decode_qk_norm_rope_append_split_paged", _p(out), _p(q),

@@ -230,7 +230,7 @@ def config3_step(ctx):
     def run():
         for s in range(steps):
             for l in range(L):
-                be.run_decode_append(outs[s, l], qs[s, l], cache.view(l), kn[s, l], vn[s, l], pos)
+                be.run_decode_append(outs[s, l], qs[s, l], cache.slabs(l), kn[s, l], vn[s, l], pos)
             R.advance_position(pos, 1)
         R.advance_position(pos, -steps)
 

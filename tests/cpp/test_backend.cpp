@@ -16,6 +16,7 @@
 #include <runtherder/attention/adaptive.h>
 #include <runtherder/attention/factory.h>
 #include <runtherder/engine/kv_cache.h>
+#include <runtherder/kernels/flash_decode.h>
 #include <runtherder/kernels/rmsnorm.h>
 #include <runtherder/kernels/rope.h>
 
@@ -27,6 +28,13 @@ using runtherder::attention::make_attention_backend;
 using runtherder::engine::KVCache;
 
 namespace {
+
+// The scratch size is a constant expression, as in the reference
+// (include/runtherder/kernels/flash_decode.cuh:16): callers size static
+// buffers with it.
+static_assert(runtherder::kernels::flash_split_scratch_floats(24, 128, 256) ==
+                  24u * 256u * 2u + 24u * 256u * 128u,
+              "flash_split_scratch_floats is constexpr and keeps the reference formula");
 
 struct Stats {
     double max_abs = 0.0;
@@ -291,7 +299,7 @@ int run_decode_step_case() {
             const uint16_t* kn = dk + static_cast<size_t>(p) * Hkv * D;
             const uint16_t* vn = dv + static_cast<size_t>(p) * Hkv * D;
             if (mode == 0) {
-                backend.run_decode_append(bf(o1), cbf(q), a.view(0), cbf(kn), cbf(vn), pos,
+                backend.run_decode_append(bf(o1), cbf(q), a.slabs(0), cbf(kn), cbf(vn), pos,
                                           nullptr);
                 b.append(0, cbf(kn), cbf(vn), 1, pos, nullptr);
                 backend.run(bf(o2), cbf(q), b.view(0), 1, pos, nullptr);
@@ -299,10 +307,10 @@ int run_decode_step_case() {
                 RUNTHERDER_HIP_CHECK(hipMemcpy(dq2, q, Hq * D * 2, hipMemcpyDeviceToDevice));
                 RUNTHERDER_HIP_CHECK(hipMemcpy(dk2, kn, Hkv * D * 2, hipMemcpyDeviceToDevice));
                 if (mode == 1) {
-                    backend.run_decode_rope_append(bf(o1), cbf(q), a.view(0), cbf(kn), cbf(vn),
+                    backend.run_decode_rope_append(bf(o1), cbf(q), a.slabs(0), cbf(kn), cbf(vn),
                                                    pos, dinv, pos, nullptr);
                 } else {
-                    backend.run_decode_qk_norm_rope_append(bf(o1), cbf(q), a.view(0), cbf(kn),
+                    backend.run_decode_qk_norm_rope_append(bf(o1), cbf(q), a.slabs(0), cbf(kn),
                                                            cbf(vn), cbf(dgq), cbf(dgk), eps, pos,
                                                            dinv, pos, nullptr);
                     runtherder::kernels::rmsnorm_bf16_forward(bf(dq2), cbf(dq2), cbf(dgq), Hq, D,

@@ -96,6 +96,24 @@ def test_cpp_headers_compile():
 static_assert(sizeof(runtherder::attention::KVView) == 6 * sizeof(void*));
 // The reference's aggregate form still builds a contiguous view.
 static_assert(runtherder::attention::KVView{nullptr, nullptr, nullptr, nullptr}.block_table == nullptr);
+// Scratch sizing is a constant expression, as in the reference
+// (flash_decode.cuh:16-24).
+static_assert(runtherder::kernels::flash_split_scratch_floats(32, 128, 64) == 32 * 64 * 130);
+// The fused decode steps take writable slabs: a read-only KVView does not
+// convert to them.
+#include <type_traits>
+static_assert(!std::is_convertible_v<runtherder::attention::KVView,
+                                     runtherder::attention::KVSlabs>);
+static_assert(std::is_invocable_v<
+    decltype(&runtherder::attention::AdaptiveAttention::run_decode_append),
+    runtherder::attention::AdaptiveAttention&, __hip_bfloat16*, const __hip_bfloat16*,
+    const runtherder::attention::KVSlabs&, const __hip_bfloat16*, const __hip_bfloat16*,
+    const int*, hipStream_t>);
+static_assert(!std::is_invocable_v<
+    decltype(&runtherder::attention::AdaptiveAttention::run_decode_append),
+    runtherder::attention::AdaptiveAttention&, __hip_bfloat16*, const __hip_bfloat16*,
+    const runtherder::attention::KVView&, const __hip_bfloat16*, const __hip_bfloat16*,
+    const int*, hipStream_t>);
 int main() { return 0; }
 """
     res = subprocess.run(["/opt/rocm/bin/hipcc", "-std=c++20", "-fsyntax-only", "-x", "hip",
@@ -133,3 +151,21 @@ def test_paged_rejects_block_sizes():
                                  None)
     assert "power of two" in _err("rth_kv_append_fp8_paged", FAKE, FAKE, FAKE, FAKE, FAKE, FAKE,
                                   FAKE, 4, 8, 128, FAKE, 100, None)
+
+
+def test_fused_decode_steps_need_writable_slabs():
+    import torch
+    cache_k = torch.zeros((4, 1, 64), dtype=torch.uint8)
+    sc = torch.zeros((4, 1), dtype=torch.float32)
+    view = R.KVView(cache_k, cache_k, sc, sc)
+    be = R.AdaptiveAttention.__new__(R.AdaptiveAttention)   # no device scratch needed
+    be.config = R.AttnConfig.for_heads(4, 1, 64)
+    for call in (lambda: be.run_decode_append(None, None, view, None, None, None),
+                 lambda: be.run_decode_rope_append(None, None, view, None, None, None, None, None),
+                 lambda: be.run_decode_qk_norm_rope_append(None, None, view, None, None, None,
+                                                           None, 1e-6, None, None, None)):
+        with pytest.raises(TypeError):
+            call()
+    slabs = R.KVSlabs(cache_k, cache_k, sc, sc)
+    v2 = slabs.view()
+    assert type(v2) is R.KVView and v2.k is cache_k and v2.block_table is None

@@ -144,7 +144,7 @@ def test_config3_28_layer_128_step_graph():
     with torch.cuda.graph(g, stream=stream):
         for s in range(steps):
             for l in range(layers):
-                backend.run_decode_append(outs[s, l], qs[s, l], cache.view(l), kn[s, l],
+                backend.run_decode_append(outs[s, l], qs[s, l], cache.slabs(l), kn[s, l],
                                           vn[s, l], pos)
             R.advance_position(pos, 1)
     pos.fill_(depth)

@@ -113,9 +113,9 @@ def test_paged_rope_decode_step(total, block, hq, hkv, d):
     step(f"paged rope decode step total={total} block={block} hq={hq} hkv={hkv} d={d}")
     o_paged = torch.empty((hq, d), dtype=torch.bfloat16, device=DEV)
     o_cont = torch.empty_like(o_paged)
-    be.run_decode_rope_append(o_paged, bf16_dev(q), paged.view(0, bt), bf16_dev(kn),
+    be.run_decode_rope_append(o_paged, bf16_dev(q), paged.slabs(0, bt), bf16_dev(kn),
                               bf16_dev(vn), posd, invd, cl)
-    be.run_decode_rope_append(o_cont, bf16_dev(q), cont.view(0), bf16_dev(kn), bf16_dev(vn),
+    be.run_decode_rope_append(o_cont, bf16_dev(q), cont.slabs(0), bf16_dev(kn), bf16_dev(vn),
                               posd, invd, cl)
     sync()
     got = bf16_host(o_paged)
@@ -234,9 +234,9 @@ def test_paged_qk_norm_rope_decode_step():
     step("paged qk-norm rope decode step")
     o_p = torch.empty((hq, d), dtype=torch.bfloat16, device=DEV)
     o_c = torch.empty_like(o_p)
-    be.run_decode_qk_norm_rope_append(o_p, q, paged.view(0, bt), kn, vn, qg, kg, eps, posd, invd,
+    be.run_decode_qk_norm_rope_append(o_p, q, paged.slabs(0, bt), kn, vn, qg, kg, eps, posd, invd,
                                       cl)
-    be.run_decode_qk_norm_rope_append(o_c, q, cont.view(0), kn, vn, qg, kg, eps, posd, invd, cl)
+    be.run_decode_qk_norm_rope_append(o_c, q, cont.slabs(0), kn, vn, qg, kg, eps, posd, invd, cl)
     sync()
     assert np.array_equal(bf16_host(o_p), bf16_host(o_c))
     gk, _, gks, _ = gather(paged, table, total, block)

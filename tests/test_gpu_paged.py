@@ -137,8 +137,8 @@ def test_paged_fused_append_decode_equals_contiguous(total, block, hq, hkv):
     o1 = torch.empty((hq, d), dtype=torch.bfloat16, device=DEV)
     o2 = torch.empty_like(o1)
     step(f"paged fused append+decode total={total} block={block}")
-    be.run_decode_append(o1, q, cont.view(0), kn, vn, int_dev(total - 1))
-    be.run_decode_append(o2, q, paged.view(0, bt), kn, vn, int_dev(total - 1))
+    be.run_decode_append(o1, q, cont.slabs(0), kn, vn, int_dev(total - 1))
+    be.run_decode_append(o2, q, paged.slabs(0, bt), kn, vn, int_dev(total - 1))
     sync()
     got = bf16_host(o2)
     assert np.array_equal(bf16_host(o1), got)

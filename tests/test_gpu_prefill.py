@@ -106,6 +106,45 @@ def test_q_rows_of_extreme_magnitude(n):
         check_rows(got, q, k8, v8, ks, vs, 0, sampled_rows(n, 12, n), hq, hkv, d, scale)
 
 
+def mixed_magnitude_q(n, hq, d, seed):
+    """Rows whose elements span ~22 binades below the row maximum: one element
+    at +-2^e (e in [-3, 5]) and the others at +-2^(e - t), t uniform in
+    [1, 22]. In the kernel's scaled units (row maximum in [128, 256)) the
+    elements below 2^-6, those more than ~13 binades under the maximum, are
+    where the two-part E4M3 split of q is not exact (error <= 2^-14 scaled,
+    tests/test_prefill_q_split.py); the large ones need the lo part."""
+    rng = np.random.default_rng(seed)
+    e = rng.integers(-3, 6, size=(n, hq, 1)).astype(np.float64)
+    t = rng.uniform(1.0, 22.0, size=(n, hq, d))
+    x = np.exp2(e - t) * rng.choice([-1.0, 1.0], size=(n, hq, d))
+    top = rng.integers(0, d, size=(n, hq))
+    np.put_along_axis(x, top[..., None], np.exp2(e) * rng.choice([-1.0, 1.0], size=(n, hq, 1)),
+                      axis=2)
+    return O.f32_to_bf16(x.astype(np.float32))
+
+
+@pytest.mark.parametrize("n", [300, 700, 4100])
+def test_q_rows_mixing_max_and_tiny_elements(n):
+    """Every row mixes its maximum with elements down to 2^-22 of it: the
+    scores come from the exact hi part, the lo part (large elements) and the
+    subnormal-limited lo part (tiny elements); the output must still match
+    the oracle's scores, which use the bf16 q as is. n 300 / 700 / 4100 run
+    the 4-wave, key-split and 8-wave workgroups (the last on sampled rows)."""
+    hq, hkv, d = (8, 2, 128) if n < 1000 else (32, 8, 128)
+    scale = np.float32(1.0 / np.sqrt(d))
+    q = mixed_magnitude_q(n, hq, d, 44)
+    k8, ks = O.quantize_kv_fp8(O.normal_bf16((n * hkv, d), 45), d)
+    v8, vs = O.quantize_kv_fp8(O.normal_bf16((n * hkv, d), 46), d)
+    got = gpu_prefill(q, k8, v8, ks, vs, n, 0, hq, hkv, d, scale)
+    assert np.isfinite(O.bf16_to_f32(got)).all()
+    if n < 1000:
+        want = O.attention_f32(q, k8, v8, ks, vs, n, 0, hq, hkv, d, scale, NTHREADS)
+        mx, mean = O.bf16_err(got, want)
+        assert mx <= MAX_ABS and mean <= MEAN_ABS, (mx, mean)
+    else:
+        check_rows(got, q, k8, v8, ks, vs, 0, sampled_rows(n, 12, n), hq, hkv, d, scale)
+
+
 @pytest.mark.parametrize("n_new,clen,hq,hkv", [
     (513, 0, 8, 2), (513, 129, 16, 4), (640, 64, 8, 8), (777, 1, 24, 8), (1500, 0, 8, 1),
 ])
