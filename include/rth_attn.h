@@ -97,13 +97,18 @@ enum {
     RTH_DECODE_VALU = 2, /* VALU split kernel (DPP / shuffle reductions) */
 };
 
-/* No counterpart in the reference: which split kernel the decode entries run
- * for this shape (RTH_DECODE_MFMA or RTH_DECODE_VALU), 0 if the shape is not
- * supported. Lets a caller or a test tell the two paths apart. */
+/* No counterpart in the reference: which split kernel rth_attn_decode_split,
+ * rth_attn_decode_split_noalloc and rth_attn_decode_append_split run for this
+ * shape (RTH_DECODE_MFMA or RTH_DECODE_VALU), 0 if the shape is not
+ * supported; it follows rth_set_decode_kernel. The paged, RoPE and q/k-norm
+ * entries always run the MFMA kernel and accept the shapes this reports as
+ * RTH_DECODE_MFMA under the automatic choice (path 0), whatever the switch. */
 int rth_decode_path(int num_q_heads, int num_kv_heads, int head_dim);
 
 /* No counterpart in the reference: process-wide choice of the split kernel
- * for the non-paged decode entries, for measurement and tuning. path 0 (the
+ * for rth_attn_decode_split, rth_attn_decode_split_noalloc and
+ * rth_attn_decode_append_split, for measurement and tuning (the paged, RoPE
+ * and q/k-norm entries ignore it). path 0 (the
  * default) = the MFMA kernel wherever it supports the shape, the VALU kernel
  * elsewhere; RTH_DECODE_VALU = the VALU kernel for every shape. Results of
  * the two kernels agree within the attention tolerance, not bit for bit.
@@ -225,8 +230,8 @@ int rth_attn_decode_append_split_paged(uint16_t* out, const uint16_t* q, uint8_t
  * positions[0] with rth_rope_bf16's arithmetic, so the cache row written at
  * *cache_len is byte-identical to rth_rope_bf16 + rth_kv_append_fp8 and the
  * output equals rth_attn_decode_append_split on the rotated q and k. Shapes
- * rth_decode_path reports as RTH_DECODE_MFMA (head_dim 64, 128, 256); others
- * fail with an error. block_table == NULL (or the first entry point): the
+ * rth_decode_path reports as RTH_DECODE_MFMA under the automatic choice
+ * (head_dim 64, 128, 256); others fail with an error. block_table == NULL (or the first entry point): the
  * contiguous layout. */
 int rth_attn_decode_rope_append_split(uint16_t* out, const uint16_t* q, uint8_t* k_cache,
                                       uint8_t* v_cache, float* k_scale, float* v_scale,

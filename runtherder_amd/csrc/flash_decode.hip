@@ -1248,7 +1248,7 @@ __global__ __launch_bounds__(kCombineThreads) void flash_decode_combine_kernel(
 // Serves the shapes the MFMA kernel does not (head_dim 32 and 512, GQA groups
 // that do not split into blocks of 4-16 q heads) with the same partition (one
 // wave per (kv head, split, block of kVGroup q heads) unit at every context;
-// kvg = -1 for the merge), the same scratch and the same merge kernel. No
+// kvg = 0 for the merge), the same scratch and the same merge kernel. No
 // MFMA: a key row of D E4M3 bytes is spread over D / 16 lanes, 16 bytes per
 // lane (one coalesced 128-bit load of K and one of V), so a wave takes
 // 64 / (D / 16) keys per step. Each lane

@@ -417,3 +417,42 @@ def test_value_magnitudes_within_f16_staging(mag):
     assert np.isfinite(a).all()
     err = np.abs(a - b)
     assert err.max() <= MAX_ABS and err.mean() <= MEAN_ABS, (err.max(), err.mean())
+
+
+def test_workgroup_shapes_agree_with_each_other():
+    """The three prefill workgroup shapes on the same heads: the key-split
+    kernel sums each row's exponentials as f16 p (v_dot2c, its register
+    budget), the 4- and 8-wave kernels as fp32 e; the P V MFMAs of all three
+    use f16 p. The heads are replicated so that one call takes each shape
+    (hq 8: key split, hq 128: 4-wave, hq 256: 8-wave); outputs of the same
+    head must agree within 2 bf16 ulps where |O| > 1e-2 and within 2e-4
+    elsewhere, and each with the oracle."""
+    n, hq0, hkv0, d = 700, 8, 2, 128
+    scale = np.float32(1.0 / np.sqrt(d))
+    q = O.normal_bf16((n, hq0, d), 51)
+    k8, ks = O.quantize_kv_fp8(O.normal_bf16((n * hkv0, d), 52), d)
+    v8, vs = O.quantize_kv_fp8(O.normal_bf16((n * hkv0, d), 53), d)
+    outs = []
+    for rep in (1, 16, 32):
+        hq, hkv = hq0 * rep, hkv0 * rep
+        qr = np.tile(q, (1, rep, 1))
+        k_r = np.tile(k8.reshape(n, hkv0, d), (1, rep, 1)).reshape(-1, d)
+        v_r = np.tile(v8.reshape(n, hkv0, d), (1, rep, 1)).reshape(-1, d)
+        ks_r = np.tile(ks.reshape(n, hkv0), (1, rep)).reshape(-1)
+        vs_r = np.tile(vs.reshape(n, hkv0), (1, rep)).reshape(-1)
+        got = gpu_prefill(qr, k_r, v_r, ks_r, vs_r, n, 0, hq, hkv, d, scale)
+        outs.append(O.bf16_to_f32(got.reshape(n, rep, hq0, d)[:, -1]))
+    want = O.attention_f32(q, k8, v8, ks, vs, n, 0, hq0, hkv0, d, scale, NTHREADS)
+    for o in outs:
+        mx, mean = O.bf16_err(O.f32_to_bf16(o), want)
+        assert mx <= MAX_ABS and mean <= MEAN_ABS, (mx, mean)
+    def ordered(x):   # bf16 bit patterns as integers ordered like the values
+        b16 = O.f32_to_bf16(x).astype(np.int32)
+        return np.where(b16 & 0x8000, 0x8000 - b16, b16)
+
+    for a in outs[1:]:
+        b = outs[0]
+        big = np.abs(b) > 1e-2
+        ulps = np.abs(ordered(a) - ordered(b))[big]
+        assert ulps.max() <= 2, ulps.max()
+        assert np.abs(a - b)[~big].max() <= 2e-4, np.abs(a - b)[~big].max()

@@ -68,3 +68,49 @@ def test_noalloc_rejects_oversized_scratch():
         _ffi.call("rth_attn_decode_split_noalloc", fake, fake, fake, fake, fake, fake, 4096,
                   fake, 64, 8, 128, scale, None)
     assert "exceeds the fixed scratch" in str(e.value)
+
+
+def test_noalloc_first_then_graph_captured():
+    """The allocation-free entry called first in this test (so its own
+    per-device set-up runs before any other entry here), then captured in a
+    HIP graph in global capture mode (where an allocation would fail the
+    capture) and replayed three times with eager work between the replays;
+    every replay equals the caller-scratch entry bit for bit."""
+    ctx, hq, hkv, d, splits = 6000, 24, 8, 128, 128
+    scale = np.float32(1.0 / np.sqrt(d))
+    q = O.normal_bf16((hq, d), 940)
+    k8, ks = O.quantize_kv_fp8(O.normal_bf16((ctx * hkv, d), 941), d)
+    v8, vs = O.quantize_kv_fp8(O.normal_bf16((ctx * hkv, d), 942), d)
+    qd, kd, vd, ksd, vsd = bf16_dev(q), u8_dev(k8), u8_dev(v8), f32_dev(ks), f32_dev(vs)
+    pos = int_dev(ctx - 1)
+    o_na = torch.empty((hq, d), dtype=torch.bfloat16, device=DEV)
+    o_ref = torch.empty_like(o_na)
+    args = lambda o, st: (_p(o), _p(qd), _p(kd), _p(vd), _p(ksd), _p(vsd), splits, _p(pos), hq,
+                          hkv, d, ctypes.c_float(scale), st)
+    step("no-alloc decode first call, then graph capture")
+    _ffi.call("rth_attn_decode_split_noalloc", *args(o_na, _stream()))
+    sync()
+    first = bf16_host(o_na)
+    part = R.new_flash_split_scratch(hq, d, splits)
+    _ffi.call("rth_attn_decode_split", _p(o_ref), _p(qd), _p(kd), _p(vd), _p(ksd), _p(vsd),
+              _p(part), splits, _p(pos), hq, hkv, d, ctypes.c_float(scale), _stream())
+    sync()
+    ref = bf16_host(o_ref)
+    assert np.array_equal(first, ref)
+    g = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(g, stream=s, capture_error_mode="global"):
+            _ffi.call("rth_attn_decode_split_noalloc",
+                      *args(o_na, ctypes.c_void_p(s.cuda_stream)))
+    torch.cuda.current_stream().wait_stream(s)
+    for rep in range(3):
+        o_na.zero_()
+        sync()
+        g.replay()
+        sync()
+        assert np.array_equal(bf16_host(o_na), ref), rep
+        # eager work on the same array between replays
+        _ffi.call("rth_attn_decode_split_noalloc", *args(o_ref, _stream()))
+        sync()
