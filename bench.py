@@ -43,6 +43,12 @@ def decode_bytes(ctx: int, hq: int, hkv: int, d: int) -> int:
     return ctx * hkv * d * 2 + ctx * hkv * 8 + hq * d * 4
 
 
+def append_bytes(hkv: int, d: int) -> int:
+    """The fused call's one-token append: k_new, v_new bf16 in, E4M3 codes
+    and fp32 scales out."""
+    return hkv * d * 2 * 2 + hkv * d * 2 + hkv * 8
+
+
 def prefill_flops(n: int, clen: int, hq: int, d: int) -> int:
     pairs = n * clen + n * (n + 1) // 2
     return 4 * hq * d * pairs
@@ -164,9 +170,11 @@ def bench_decode(torch, R, args, stream):
     value_gbs = total_bytes / (timed[True] * 1e-3) / 1e9
     unfused_gbs = total_bytes / (timed[False] * 1e-3) / 1e9
 
-    # Dominant kernels alone: one decode call (split kernel + merge kernel) per
-    # layer, rotating over the 28 layers (defeats the 256 MB Infinity Cache),
-    # captured back to back in a graph and timed with HIP events on its stream.
+    # Dominant kernels alone: the headline step's call (the fused K/V append +
+    # split kernel, then the merge kernel) once per layer, rotating over the
+    # 28 layers (defeats the 256 MB Infinity Cache), captured back to back in
+    # a graph and timed with HIP events on its stream. Every call appends at
+    # row `depth` (rewritten each time) and attends to depth + 1 keys.
     n_launch = L * 20
     kgraph = torch.cuda.CUDAGraph()
     with torch.cuda.stream(stream):
@@ -175,14 +183,15 @@ def bench_decode(torch, R, args, stream):
         with torch.cuda.graph(kgraph, stream=stream):
             for i in range(n_launch):
                 l = i % L
-                backend.run(out[0, l], qs[0, l], cache.view(l), 1, pos)
+                backend.run_decode_append(out[0, l], qs[0, l], cache.slabs(l), ks[0, l],
+                                          vs[0, l], pos)
         kgraph.replay()
         torch.cuda.synchronize()
         with EventTimer(torch, stream) as tk:
             kgraph.replay()
     torch.cuda.synchronize()
     kern_us = tk.ms * 1e3 / n_launch
-    kbytes = decode_bytes(depth + 1, hq, hkv, d)
+    kbytes = decode_bytes(depth + 1, hq, hkv, d) + append_bytes(hkv, d)
     achieved = kbytes / (kern_us * 1e-6) / 1e9
 
     # The same steps with RoPE in them (the engine's per-layer sequence
@@ -351,9 +360,11 @@ def bench_rope_append(torch, R, stream, n=4096, iters=20):
 
 
 def decode_kernel_sweep(torch, R, stream, points, quiet=False):
-    """Per-call decode time (split kernel + merge kernel) at several context
+    """Per-call decode time of the headline step's call (the fused one-token
+    K/V append + split kernel, then the merge kernel) at several context
     depths, rotating over enough layers that the working set exceeds the
-    256 MB Infinity Cache. points: (hq, hkv, ctx, splits or None)."""
+    256 MB Infinity Cache; every call appends at row ctx - 1 (rewritten each
+    time) and attends to ctx keys. points: (hq, hkv, ctx, splits or None)."""
     res = []
     d = 128
     dev = torch.device("cuda:0")
@@ -368,6 +379,7 @@ def decode_kernel_sweep(torch, R, stream, points, quiet=False):
         backend = R.AdaptiveAttention(R.AttnConfig(hq, hkv, d, 1.0 / math.sqrt(d)),
                                       num_splits=splits)
         q = torch.randn((L, hq, d), device=dev).to(torch.bfloat16)
+        kn = torch.randn((L, hkv, d), device=dev).to(torch.bfloat16)
         out = torch.empty((L, hq, d), dtype=torch.bfloat16, device=dev)
         pos = torch.full((1,), ctx - 1, dtype=torch.int32, device=dev)
         n = L * max(2, math.ceil(200 / L))
@@ -376,20 +388,21 @@ def decode_kernel_sweep(torch, R, stream, points, quiet=False):
             g = torch.cuda.CUDAGraph()
             with torch.cuda.graph(g, stream=stream):
                 for i in range(n):
-                    backend.run(out[i % L], q[i % L], cache.view(i % L), 1, pos)
+                    backend.run_decode_append(out[i % L], q[i % L], cache.slabs(i % L),
+                                              kn[i % L], kn[i % L], pos)
             g.replay()
             torch.cuda.synchronize()
             with EventTimer(torch, stream) as t:
                 g.replay()
         torch.cuda.synchronize()
         us = t.ms * 1e3 / n
-        nbytes = decode_bytes(ctx, hq, hkv, d)
+        nbytes = decode_bytes(ctx, hq, hkv, d) + append_bytes(hkv, d)
         res.append({"hq": hq, "hkv": hkv, "ctx": ctx, "splits": backend.num_splits,
                     "layers": L, "us": round(us, 2), "gbs": round(nbytes / us / 1e3, 1),
                     "frac": round(nbytes / us / 1e3 / PEAK_HBM_GBS, 4)})
         if not quiet:
             print(json.dumps({"decode_sweep": res[-1]}), flush=True)
-        del cache, backend, q, out
+        del cache, backend, q, kn, out
         torch.cuda.empty_cache()
     return res
 
@@ -444,6 +457,9 @@ def eager_kernels(torch, R, stream, args):
     with torch.cuda.stream(stream):
         for i in range(2 * L):
             l = i % L
+            if args.fused:
+                backend.run_decode_append(out[l], q[l], cache.slabs(l), kn[l], kn[l], pos)
+                continue
             if i < L:
                 cache.append(l, kn[l], kn[l], 1, pos)
             backend.run(out[l], q[l], cache.view(l), 1, pos)
@@ -564,12 +580,13 @@ def extra_rooflines(torch, R, stream):
                                       (32, 8, 131072, 64, "config5"),
                                       (32, 8, 131072, None, "config5 default splits")):
         pt = decode_kernel_sweep(torch, R, stream, [(hq, hkv, ctx, splits)], quiet=True)[0]
-        out.append({"kind": "decode", "workload": f"{cfg}: decode {hq}Q/{hkv}KV ctx {ctx}, "
-                                                  f"{pt['splits']} splits",
+        out.append({"kind": "decode", "workload": f"{cfg}: fused one-token append + decode "
+                                                  f"{hq}Q/{hkv}KV ctx {ctx}, {pt['splits']} splits",
                     "us": pt["us"],
                     "roofline": {"bound": "hbm", "achieved": pt["gbs"], "peak": PEAK_HBM_GBS,
                                  "unit": "GB/s", "frac": pt["frac"],
-                                 "bytes_per_launch": decode_bytes(ctx, hq, hkv, 128),
+                                 "bytes_per_launch": decode_bytes(ctx, hq, hkv, 128)
+                                 + append_bytes(hkv, 128),
                                  "traffic": (profile_traffic("decode_attn_128k_pmc_traffic.md")
                                              if (ctx == 131072 and splits == 64) else None)}})
     for n in (8192, 16384):
@@ -595,6 +612,9 @@ def main() -> int:
     ap.add_argument("--splits", type=int, default=None,
                     help="--mode kernels: decode split count (default: the backend's)")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--fused", action="store_true",
+                    help="--mode kernels: decode calls through the fused append + decode entry "
+                         "(the headline step's call) instead of append then run")
     ap.add_argument("--decode-kernel", choices=("auto", "valu"), default="auto",
                     help="valu: run every decode call on the VALU split kernel (A/B against "
                          "the MFMA kernel with --mode kernels or --sweep decode)")
@@ -663,7 +683,7 @@ def main() -> int:
             "bound": "hbm", "achieved": round(dec["kernel_gbs"], 1), "peak": PEAK_HBM_GBS,
             "unit": "GB/s", "frac": round(dec["kernel_gbs"] / PEAK_HBM_GBS, 4),
             "traffic": profile_traffic(),
-            "kernel": "flash_decode_kernel<128> + flash_decode_combine_kernel<128> (one call)",
+            "kernel": "flash_decode_kernel<128, true, false> + flash_decode_combine_kernel<128> (one fused append + decode call)",
             "kernel_us": round(dec["kernel_us"], 3), "bytes_per_launch": dec["kernel_bytes"],
         },
         "prefill": {
