@@ -133,6 +133,47 @@ __device__ __forceinline__ void load_tile(TileRaw<D>& t, const uint8_t* __restri
     constexpr int kRpi  = kWave / kCpr;    // rows per load instruction
     const int     rr    = lane / kCpr;
     const int     ch    = lane % kCpr;
+    if (!kNT && kb + kTileKeys <= k1) {
+        // A full tile of a short (latency-bound) stream: wave-uniform row
+        // bases (scalar) plus per-lane 32-bit offsets that do not change from
+        // tile to tile, so the addresses cost no per-tile vector arithmetic
+        // (8K: 12.38 -> 12.12 us per call; the nontemporal streams of longer
+        // contexts measured 0.3-0.4 us slower with it at 128K and keep the
+        // clamped per-row addresses below).
+        const int64_t  rs = static_cast<int64_t>(hkv) * D;   // bytes per token row
+        const uint8_t* kt = k + (static_cast<int64_t>(kb + delta) * hkv + kvh) * D;
+        const uint8_t* vt = v + (static_cast<int64_t>(kb + delta) * hkv + kvh) * D;
+#pragma unroll
+        for (int i = 0; i < kTileKeys / kRpi; ++i) {
+            const int      r   = i * kRpi + rr;
+            const uint32_t off = static_cast<uint32_t>(r * rs) + 16u * (ch ^ k_swz<D>(r));
+            t.kraw[i / T::kKChunks][i % T::kKChunks] =
+                ld<kNT>(reinterpret_cast<const u32x4*>(kt + off));
+        }
+        const int n = lane & 15;
+        const int g = lane >> 4;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const uint32_t off = static_cast<uint32_t>(key_of(g, j) * rs) + T::kVBytes * n;
+            if constexpr (T::kVWords == 1) {
+                t.vraw[j][0] = ld<kNT>(reinterpret_cast<const uint32_t*>(vt + off));
+            } else if constexpr (T::kVWords == 2) {
+                const u32x2 w = ld<kNT>(reinterpret_cast<const u32x2*>(vt + off));
+                t.vraw[j][0]  = w.x;
+                t.vraw[j][1]  = w.y;
+            } else {
+                const u32x4 w = ld<kNT>(reinterpret_cast<const u32x4*>(vt + off));
+                t.vraw[j][0]  = w.x;
+                t.vraw[j][1]  = w.y;
+                t.vraw[j][2]  = w.z;
+                t.vraw[j][3]  = w.w;
+            }
+        }
+        const int64_t srow = static_cast<int64_t>(kb + delta) * hkv + kvh;
+        const float*  sp   = (lane < 32) ? ks + srow : vs + srow;
+        t.sc               = sp[(lane & 31) * hkv];
+        return;
+    }
 #pragma unroll
     for (int i = 0; i < kTileKeys / kRpi; ++i) {
         const int      r   = i * kRpi + rr;
@@ -647,8 +688,10 @@ __device__ __forceinline__ void decode_body(
         rope_sync();
         return;
     }
-    const int kvc = kvh / nqb;   // cache kv head
-    const int hkc = hkv / nqb;   // cache kv heads
+    // Wave-uniform by construction; kept in scalar registers so that tile
+    // addresses are a scalar base plus fixed per-lane offsets.
+    const int kvc = __builtin_amdgcn_readfirstlane(kvh / nqb);   // cache kv head
+    const int hkc = __builtin_amdgcn_readfirstlane(hkv / nqb);   // cache kv heads
     // The appended row's bf16 words, issued before the stream (D <= 128: the
     // 40 VGPRs they hold through the stream spill the D = 256 kernels). Plain
     // loads, not loads inside the owner branch: a branch-merged load makes the
@@ -803,7 +846,7 @@ __device__ __forceinline__ void decode_body(
 
     constexpr float kLazy = 8.0f;
     auto process = [&](const TileRaw<D>& cur, const int kb, const int klim) {
-        sm_sc[wave][lane] = cur.sc;
+        sm_sc[wave][lane] = (lane < 32) ? cur.sc * scale_log2 : cur.sc;   // k-factors pre-scaled
         __builtin_amdgcn_wave_barrier();
         // S^T = K Q^T, two 16-key halves.
         f32x4 s[2];
@@ -828,8 +871,8 @@ __device__ __forceinline__ void decode_body(
         float x[8];
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-            x[r]     = s[0][r] * (kf0[r] * scale_log2);
-            x[4 + r] = s[1][r] * (kf1[r] * scale_log2);
+            x[r]     = s[0][r] * kf0[r];
+            x[4 + r] = s[1][r] * kf1[r];
         }
         if (kb + kTileKeys > klim) {  // ragged last tile of the split
 #pragma unroll
@@ -1002,7 +1045,7 @@ __device__ __forceinline__ void decode_body(
                     M = fmaxf(M, sm_m[kl + j * pt.gkv][n]);
                 }
             }
-            const float wf = (m_run == -INFINITY) ? 0.0f : exp2f(m_run - M);
+            const float wf = (m_run == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(m_run - M);
 #pragma unroll
             for (int c = 0; c < T::kOMfma; ++c) {
 #pragma unroll
@@ -1043,7 +1086,7 @@ __device__ __forceinline__ void decode_body(
             for (int j = 0; j < kDecWaves; ++j) {
                 if (j < wpk) {
                     const float mw = sm_m[el + j * pt.gkv][h];
-                    L += (mw == -INFINITY) ? 0.0f : sm_l[el + j * pt.gkv][h] * exp2f(mw - M);
+                    L += (mw == -INFINITY) ? 0.0f : sm_l[el + j * pt.gkv][h] * __builtin_amdgcn_exp2f(mw - M);
                 }
             }
             const int64_t slot = static_cast<int64_t>((kvh0 + el) * G + h) * num_splits + si;
@@ -1127,13 +1170,16 @@ __global__ __launch_bounds__(kDecThreads) void flash_decode_qk_norm_rope_kernel(
 
 // One workgroup per (q head, 16-wide slice of head_dim): merges the n_eff
 // split partials, out = sum_s 2^(m_s - M) acc_s / sum_s 2^(m_s - M) l_s
-// (reference src/kernels/flash_decode.cu:222-247). Thread (group grp, quad
-// qd) folds splits grp, grp + kGroups, ... for d = 4qd .. 4qd+3 of the slice
-// with an online max, eight loads in flight at a time. Its first eight loads
-// are issued before the split count is known (slot indices clamped into the
-// scratch), so they share one round trip with the read of *cache_len; slots
-// no split wrote in this call are dropped by a select. The group states
-// then merge by lane exchanges inside each wave and once through LDS.
+// (reference src/kernels/flash_decode.cu:222-247), in two passes so that no
+// exponential sits in a reduction tree: every wave first takes M, the
+// maximum of the head's live m_s, from the m row itself (four coalesced
+// loads per lane for up to 256 splits, a wave reduction); then thread (group grp,
+// quad qd) sums 2^(m_s - M) l_s and 2^(m_s - M) acc_s for splits grp,
+// grp + kGroups, ... and d = 4qd .. 4qd+3 of the slice (weights <= 1, eight
+// loads in flight), and the sums add up by lane exchanges and one LDS step.
+// The first loads are issued before the split count is known (slot indices
+// clamped into the scratch), so they share one round trip with the read of
+// *cache_len; slots no split wrote in this call are dropped by a select.
 template <int D>
 __global__ __launch_bounds__(kCombineThreads) void flash_decode_combine_kernel(
     uint16_t* __restrict__ out, const float* __restrict__ partial, int num_splits,
@@ -1143,7 +1189,7 @@ __global__ __launch_bounds__(kCombineThreads) void flash_decode_combine_kernel(
     constexpr int kCWaves = kCombineThreads / kWave;
     static_assert((kQuads & (kQuads - 1)) == 0 && kQuads <= kWave, "lane = kQuads * group + quad");
     __shared__ __attribute__((aligned(16))) f32x4 sm_acc[kCWaves][kQuads];
-    __shared__ float sm_mm[kCWaves], sm_ll[kCWaves];
+    __shared__ float sm_ll[kCWaves];
 
     const int qh   = static_cast<int>(blockIdx.x);
     const int dsl  = static_cast<int>(blockIdx.y) * kCombineSlice;
@@ -1170,62 +1216,67 @@ __global__ __launch_bounds__(kCombineThreads) void flash_decode_combine_kernel(
             os[u]       = *reinterpret_cast<const f32x4*>(&part_o[static_cast<int64_t>(s) * D + 4 * qd]);
         }
     };
-    float m = -INFINITY, l = 0.0f;
-    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-    // Folds the loaded slots below n_eff; the others may hold anything (NaN
-    // included), so they are selected away, never multiplied by zero.
-    auto fold = [&](int s0, int n_eff) {
-        float mv[8];
-        float mx = m;
+    load8(grp, num_splits - 1);
+    // The m row for M: slots lane + 64 e, e < 4 (then the next 256, ...).
+    float mr[4];
 #pragma unroll
-        for (int u = 0; u < 8; ++u) {
-            mv[u] = (s0 + u * kGroups < n_eff) ? ms[u] : -INFINITY;
-            mx    = fmaxf(mx, mv[u]);
+    for (int e = 0; e < 4; ++e) {
+        mr[e] = part_m[min(lane + kWave * e, num_splits - 1)];
+    }
+    const int n_keys = *cache_len + 1;
+    const int n_eff  = dec_partition(n_keys, num_splits, kvg).n_eff;
+    float     M      = -INFINITY;
+    for (int s0 = 0;; s0 += 4 * kWave) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            if (s0 + lane + kWave * e < n_eff) {
+                M = fmaxf(M, mr[e]);
+            }
         }
-        const float c = (m == -INFINITY) ? 0.0f : exp2f(m - mx);
-        acc *= c;
-        l *= c;
+        if (s0 + 4 * kWave >= n_eff) {
+            break;
+        }
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            mr[e] = part_m[min(s0 + 4 * kWave + lane + kWave * e, num_splits - 1)];
+        }
+    }
+#pragma unroll
+    for (int mask = 1; mask < kWave; mask <<= 1) {
+        M = fmaxf(M, wave_xor_partner(M, mask));
+    }
+
+    float l   = 0.0f;
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    // Adds the loaded slots below n_eff; the others may hold anything (NaN
+    // included), so they are selected away, never multiplied by zero.
+    auto fold = [&](int s0) {
 #pragma unroll
         for (int u = 0; u < 8; ++u) {
-            const bool  live = mv[u] != -INFINITY;
-            const float f    = live ? exp2f(mv[u] - mx) : 0.0f;
+            const bool  live = s0 + u * kGroups < n_eff;
+            const float f    = live ? __builtin_amdgcn_exp2f(ms[u] - M) : 0.0f;
             const f32x4 o    = live ? os[u] : f32x4{0.f, 0.f, 0.f, 0.f};
             acc += o * f;
             l += (live ? ls[u] : 0.0f) * f;
         }
-        m = mx;
     };
-    load8(grp, num_splits - 1);
-    const int n_keys = *cache_len + 1;
-    const int n_eff  = dec_partition(n_keys, num_splits, kvg).n_eff;
-    fold(grp, n_eff);
+    fold(grp);
     for (int s0 = grp + 8 * kGroups; s0 < n_eff; s0 += 8 * kGroups) {
         load8(s0, n_eff - 1);
-        fold(s0, n_eff);
+        fold(s0);
     }
-
-    auto merge = [&](float m2, float l2, f32x4 a2) {
-        const float M  = fmaxf(m, m2);
-        const float f1 = (m == -INFINITY) ? 0.0f : exp2f(m - M);
-        const float f2 = (m2 == -INFINITY) ? 0.0f : exp2f(m2 - M);
-        acc            = acc * f1 + a2 * f2;
-        l              = l * f1 + l2 * f2;
-        m              = M;
-    };
     // The groups of a wave differ in the lane bits above the quad index.
 #pragma unroll
     for (int mask = kQuads; mask < kWave; mask <<= 1) {
-        f32x4 a2;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-            a2[e] = wave_xor_partner(acc[e], mask);
+            acc[e] += wave_xor_partner(acc[e], mask);
         }
-        merge(wave_xor_partner(m, mask), wave_xor_partner(l, mask), a2);
+        l += wave_xor_partner(l, mask);
     }
     if (lane < kQuads) {
         sm_acc[wave][lane] = acc;
         if (lane == 0) {
-            sm_mm[wave] = m;
             sm_ll[wave] = l;
         }
     }
@@ -1233,7 +1284,8 @@ __global__ __launch_bounds__(kCombineThreads) void flash_decode_combine_kernel(
     if (wave == 0 && lane < kQuads) {
 #pragma unroll
         for (int w = 1; w < kCWaves; ++w) {
-            merge(sm_mm[w], sm_ll[w], sm_acc[w][lane]);
+            acc += sm_acc[w][lane];
+            l += sm_ll[w];
         }
         const float inv = 1.0f / l;
         u32x2       w2;
@@ -1243,8 +1295,6 @@ __global__ __launch_bounds__(kCombineThreads) void flash_decode_combine_kernel(
     }
 }
 
-
-// ---- VALU split kernel -------------------------------------------------------
 // Serves the shapes the MFMA kernel does not (head_dim 32 and 512, GQA groups
 // that do not split into blocks of 4-16 q heads) with the same partition (one
 // wave per (kv head, split, block of kVGroup q heads) unit at every context;

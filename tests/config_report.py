@@ -9,6 +9,7 @@ from __future__ import annotations
 
 import json
 import math
+import os
 import sys
 import time
 from pathlib import Path
@@ -24,7 +25,25 @@ import oracle_lib as O  # noqa: E402
 import runtherder_amd as R  # noqa: E402
 
 DEV = "cuda:0"
-THREADS = 16
+
+
+def usable_cores():
+    """Every core this process may run on (the affinity mask), capped by a
+    cgroup CPU quota when one is set, and by the oracle's 256-thread limit."""
+    try:
+        n = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        n = os.cpu_count() or 1
+    try:
+        q, period = Path("/sys/fs/cgroup/cpu.max").read_text().split()[:2]
+        if q != "max":
+            n = min(n, max(1, int(q) // int(period)))
+    except (OSError, ValueError):
+        pass
+    return max(1, min(n, 256))
+
+
+THREADS = usable_cores()
 PEAK_HBM, PEAK_MFMA = 8000.0, 2500.0
 
 
@@ -270,7 +289,7 @@ def main():
     decode_case("5: decode 128K, 64 splits, per-head scales", 131072, 32, 8, 128, 64,
                 per_head=True)
     prefill_case("5: chunk 4096 @ 126976", 4096, 126976, 32, 8, 128, block=64)
-    lines = ["| config | CPU ms (16 threads) | CPU rate | GPU us | GPU rate | % of peak | "
+    lines = [f"| config | CPU ms ({THREADS} threads, nproc {os.cpu_count()}) | CPU rate | GPU us | GPU rate | % of peak | "
              "parity (max / mean abs) |", "|---|---|---|---|---|---|---|"]
     for r in rows:
         dec = r["unit"] == "GB/s"
