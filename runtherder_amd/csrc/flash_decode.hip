@@ -1168,6 +1168,33 @@ __global__ __launch_bounds__(kDecThreads) void flash_decode_qk_norm_rope_kernel(
                                              inv_freq, q_norm, k_norm, eps);
 }
 
+// Maximum over the whole wave, every lane ending with it: DPP exchanges
+// inside each 16-lane row (quad xor 1, xor 2, half-row and row mirrors),
+// then the two cross-row swaps; no LDS traffic.
+template <int kCtrl>
+__device__ __forceinline__ float dpp_f(float x) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), kCtrl, 0xF, 0xF, false));
+}
+
+__device__ __forceinline__ float wave_max_all(float v) {
+    v = fmaxf(v, dpp_f<0xB1>(v));    // quad_perm [1,0,3,2]
+    v = fmaxf(v, dpp_f<0x4E>(v));    // quad_perm [2,3,0,1]
+    v = fmaxf(v, dpp_f<0x141>(v));   // row_half_mirror
+    v = fmaxf(v, dpp_f<0x140>(v));   // row_mirror
+    v = fmaxf(v, wave_xor_partner(v, 16));
+    return fmaxf(v, wave_xor_partner(v, 32));
+}
+
+// Sum over the lanes of a wave that share lane % 4 (the four-lane quads of
+// the merge's groups): rotations by 4 and 8 inside each 16-lane row, then
+// the two cross-row swaps.
+__device__ __forceinline__ float quad_group_sum(float v) {
+    v += dpp_f<0x124>(v);   // row_ror:4
+    v += dpp_f<0x128>(v);   // row_ror:8
+    v += wave_xor_partner(v, 16);
+    return v + wave_xor_partner(v, 32);
+}
+
 // One workgroup per (q head, 16-wide slice of head_dim): merges the n_eff
 // split partials, out = sum_s 2^(m_s - M) acc_s / sum_s 2^(m_s - M) l_s
 // (reference src/kernels/flash_decode.cu:222-247), in two passes so that no
@@ -1241,10 +1268,7 @@ __global__ __launch_bounds__(kCombineThreads) void flash_decode_combine_kernel(
             mr[e] = part_m[min(s0 + 4 * kWave + lane + kWave * e, num_splits - 1)];
         }
     }
-#pragma unroll
-    for (int mask = 1; mask < kWave; mask <<= 1) {
-        M = fmaxf(M, wave_xor_partner(M, mask));
-    }
+    M = wave_max_all(M);
 
     float l   = 0.0f;
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
@@ -1266,14 +1290,12 @@ __global__ __launch_bounds__(kCombineThreads) void flash_decode_combine_kernel(
         fold(s0);
     }
     // The groups of a wave differ in the lane bits above the quad index.
+    static_assert(kQuads == 4, "quad_group_sum sums the lanes sharing lane % 4");
 #pragma unroll
-    for (int mask = kQuads; mask < kWave; mask <<= 1) {
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            acc[e] += wave_xor_partner(acc[e], mask);
-        }
-        l += wave_xor_partner(l, mask);
+    for (int e = 0; e < 4; ++e) {
+        acc[e] = quad_group_sum(acc[e]);
     }
+    l = quad_group_sum(l);
     if (lane < kQuads) {
         sm_acc[wave][lane] = acc;
         if (lane == 0) {
@@ -1287,7 +1309,7 @@ __global__ __launch_bounds__(kCombineThreads) void flash_decode_combine_kernel(
             acc += sm_acc[w][lane];
             l += sm_ll[w];
         }
-        const float inv = 1.0f / l;
+        const float inv = __builtin_amdgcn_rcpf(l);   // 1 ulp; the output is bf16
         u32x2       w2;
         w2.x = pack_bf16x2(acc[0] * inv, acc[1] * inv);
         w2.y = pack_bf16x2(acc[2] * inv, acc[3] * inv);
