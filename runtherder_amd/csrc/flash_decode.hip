@@ -1185,10 +1185,15 @@ __device__ __forceinline__ float wave_max_all(float v) {
     return fmaxf(v, wave_xor_partner(v, 32));
 }
 
-// Sum over the lanes of a wave that share lane % 4 (the four-lane quads of
-// the merge's groups): rotations by 4 and 8 inside each 16-lane row, then
-// the two cross-row swaps.
+// Sum over the lanes of a wave that share lane % kQuads (the merge's
+// groups of kQuads lanes): rotations inside each 16-lane row, then the two
+// cross-row swaps.
+template <int kQuads>
 __device__ __forceinline__ float quad_group_sum(float v) {
+    static_assert(kQuads == 2 || kQuads == 4, "groups of 2 or 4 lanes");
+    if constexpr (kQuads == 2) {
+        v += dpp_f<0x122>(v);   // row_ror:2
+    }
     v += dpp_f<0x124>(v);   // row_ror:4
     v += dpp_f<0x128>(v);   // row_ror:8
     v += wave_xor_partner(v, 16);
@@ -1290,12 +1295,11 @@ __global__ __launch_bounds__(kCombineThreads) void flash_decode_combine_kernel(
         fold(s0);
     }
     // The groups of a wave differ in the lane bits above the quad index.
-    static_assert(kQuads == 4, "quad_group_sum sums the lanes sharing lane % 4");
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-        acc[e] = quad_group_sum(acc[e]);
+        acc[e] = quad_group_sum<kQuads>(acc[e]);
     }
-    l = quad_group_sum(l);
+    l = quad_group_sum<kQuads>(l);
     if (lane < kQuads) {
         sm_acc[wave][lane] = acc;
         if (lane == 0) {
