@@ -627,8 +627,14 @@ __device__ __forceinline__ void decode_body(
     const int wpk = kDecWaves / pt.gkv;   // coop: waves per kv head
     if (!pt.coop) {
         const int unit = bid * kDecWaves + wave;
-        kvh            = unit % hkv;
-        si             = unit / hkv;
+        // hkv is a power of two in every common shape: shifts, not divisions.
+        if ((hkv & (hkv - 1)) == 0) {
+            kvh = unit & (hkv - 1);
+            si  = unit >> __builtin_ctz(hkv);
+        } else {
+            kvh = unit % hkv;
+            si  = unit / hkv;
+        }
     } else {
         const int groups = hkv / pt.gkv;
         int       grp;
@@ -690,8 +696,8 @@ __device__ __forceinline__ void decode_body(
     }
     // Wave-uniform by construction; kept in scalar registers so that tile
     // addresses are a scalar base plus fixed per-lane offsets.
-    const int kvc = __builtin_amdgcn_readfirstlane(kvh / nqb);   // cache kv head
-    const int hkc = __builtin_amdgcn_readfirstlane(hkv / nqb);   // cache kv heads
+    const int kvc = __builtin_amdgcn_readfirstlane(nqb == 1 ? kvh : kvh / nqb);   // cache kv head
+    const int hkc = __builtin_amdgcn_readfirstlane(nqb == 1 ? hkv : hkv / nqb);   // cache kv heads
     // The appended row's bf16 words, issued before the stream (D <= 128: the
     // 40 VGPRs they hold through the stream spill the D = 256 kernels). Plain
     // loads, not loads inside the owner branch: a branch-merged load makes the
@@ -727,8 +733,8 @@ __device__ __forceinline__ void decode_body(
     // share (floor(j n / wpk) .. floor((j + 1) n / wpk) - 1).
     const int  wj        = pt.coop ? wave / pt.gkv : 0;
     const int  wn        = pt.coop ? wpk : 1;
-    const int  t_first   = (wj * n_tiles) / wn;
-    const int  last_tile = ((wj + 1) * n_tiles) / wn - 1;
+    const int  t_first   = pt.coop ? (wj * n_tiles) / wn : 0;
+    const int  last_tile = pt.coop ? ((wj + 1) * n_tiles) / wn - 1 : n_tiles - 1;
 
     // Q^T as the B operand: column n = q head n of the group. Columns past
     // G repeat head 0: their scores only ever mirror head 0's (so they never
@@ -888,11 +894,14 @@ __device__ __forceinline__ void decode_body(
             lmax              = wave_xor_max(lmax, 16);
             lmax              = wave_xor_max(lmax, 32);
             const float m_new = fmaxf(m_run, lmax);
-            const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
-            l_run *= alpha;
+            // A wave's first tile (nothing accumulated yet) needs no rescale.
+            if (!__all(m_run == -INFINITY)) {
+                const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+                l_run *= alpha;
 #pragma unroll
-            for (int c = 0; c < T::kOMfma; ++c) {
-                oacc[c] *= alpha;
+                for (int c = 0; c < T::kOMfma; ++c) {
+                    oacc[c] *= alpha;
+                }
             }
             m_run = m_new;
         }
