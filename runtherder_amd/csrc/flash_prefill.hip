@@ -465,12 +465,15 @@ __global__ __launch_bounds__(kWaves * kWave, kSplit ? 1 : 2) void flash_prefill_
             }
         }
         if ((key0 + kBN - 1 > clen + wq0) || (key0 + kBN > total)) {
+            // Key kp is visible iff kp <= min(my_pos, total - 1): one compare
+            // of the tile offset (a constant per register) against a per-lane
+            // threshold.
+            const int lim = min(my_pos, total - 1) - key0 - 4 * h;
 #pragma unroll
             for (int kb = 0; kb < 2; ++kb) {
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
-                    const int kp = key0 + 32 * kb + 8 * (r >> 2) + 4 * h + (r & 3);
-                    if (kp > my_pos || kp >= total) {
+                    if (32 * kb + 8 * (r >> 2) + (r & 3) > lim) {
                         sx[kb][r] = -INFINITY;
                     }
                 }
