@@ -133,13 +133,14 @@ __device__ __forceinline__ void load_tile(TileRaw<D>& t, const uint8_t* __restri
     constexpr int kRpi  = kWave / kCpr;    // rows per load instruction
     const int     rr    = lane / kCpr;
     const int     ch    = lane % kCpr;
-    if (!kNT && kb + kTileKeys <= k1) {
+    if (!kNT && D <= 128 && kb + kTileKeys <= k1) {
         // A full tile of a short (latency-bound) stream: wave-uniform row
         // bases (scalar) plus per-lane 32-bit offsets that do not change from
         // tile to tile, so the addresses cost no per-tile vector arithmetic
         // (8K: 12.38 -> 12.12 us per call; the nontemporal streams of longer
-        // contexts measured 0.3-0.4 us slower with it at 128K and keep the
-        // clamped per-row addresses below).
+        // contexts measured 0.3-0.4 us slower with it at 128K, and at head_dim
+        // 256 the fixed offsets spill; both keep the clamped per-row
+        // addresses below).
         const int64_t  rs = static_cast<int64_t>(hkv) * D;   // bytes per token row
         const uint8_t* kt = k + (static_cast<int64_t>(kb + delta) * hkv + kvh) * D;
         const uint8_t* vt = v + (static_cast<int64_t>(kb + delta) * hkv + kvh) * D;
@@ -953,6 +954,27 @@ __device__ __forceinline__ void decode_body(
     // cost 0.5 us per call at 2K), while the paged kernels keep issuing the
     // clamped reload (measured per call with a shuffled block table: 8K
     // 13.2 us with it vs 15.1 without, 128K 50.4 vs 51.3, 2K 9.6 vs 9.3).
+    // The appended key (owner waves): quantized, stored and attended to.
+    // kEarlyKey: right behind the first tile's loads, so that the work
+    // overlaps their latency instead of trailing the stream (the RoPE /
+    // q-k-norm kernels and head_dim 256 do it after the stream: earlier, they
+    // spill).
+    constexpr bool kEarlyKey = kAppend && !kRope && D <= 128;
+    auto new_key = [&]() __attribute__((always_inline)) {
+    if (kAppend && virt) {
+        TileRaw<D>    vt;
+        const int     prow = kPaged ? paged_row(p_new, block_table, block_shift) : p_new;
+        const int64_t row  = static_cast<int64_t>(prow) * hkc + kvc;
+        quantize_new_token<D>(vt, k_new + static_cast<int64_t>(kvc) * D,
+                              v_new + static_cast<int64_t>(kvc) * D, k_w + row * D,
+                              v_w + row * D, ks_w + row, vs_w + row, lane, kvh == kvc * nqb,
+                              kRope ? sm_rope : nullptr, kRope ? sm_rope + D / 2 : nullptr,
+                              kNorm ? sm_gain + kMaxD : nullptr, eps,
+                              (kAppend && !kNorm && D <= 128) ? pre_k : nullptr,
+                              (kAppend && !kNorm && D <= 128) ? pre_v : nullptr);
+        process(vt, p_new, p_new + 1);
+    }
+    };
     constexpr int kRing     = DecTraits<D>::kRing;
     if (t_first <= last_tile) {
         auto tile_delta = [&](int kb) {
@@ -975,6 +997,9 @@ __device__ __forceinline__ void decode_body(
                 load(ring[r], k0 + min(t_first + r, last_tile) * kTileKeys);
             }
             rope_q();   // behind the first tile loads
+            if constexpr (kEarlyKey) {
+                new_key();
+            }
             for (int t = t_first;; t += kRing) {
                 bool done = false;
 #pragma unroll
@@ -1009,20 +1034,13 @@ __device__ __forceinline__ void decode_body(
         }
     } else {
         rope_q();
+        if constexpr (kEarlyKey) {
+            new_key();
+        }
     }
 
-    if (kAppend && virt) {
-        TileRaw<D>    vt;
-        const int     prow = kPaged ? paged_row(p_new, block_table, block_shift) : p_new;
-        const int64_t row  = static_cast<int64_t>(prow) * hkc + kvc;
-        quantize_new_token<D>(vt, k_new + static_cast<int64_t>(kvc) * D,
-                              v_new + static_cast<int64_t>(kvc) * D, k_w + row * D,
-                              v_w + row * D, ks_w + row, vs_w + row, lane, kvh == kvc * nqb,
-                              kRope ? sm_rope : nullptr, kRope ? sm_rope + D / 2 : nullptr,
-                              kNorm ? sm_gain + kMaxD : nullptr, eps,
-                              (kAppend && !kNorm && D <= 128) ? pre_k : nullptr,
-                              (kAppend && !kNorm && D <= 128) ? pre_v : nullptr);
-        process(vt, p_new, p_new + 1);
+    if constexpr (!kEarlyKey) {
+        new_key();
     }
 
     // ---- partial of this split, reference layout: m at [h*S + si] (log2

@@ -4,8 +4,10 @@ sequence rope_bf16 -> KVCache::append -> AttentionBackend::run of reference
 src/model/supported/llama/llama3.cu:228-234).
 
 Checked against the GPU's own two-step sequence (rth_rope_bf16 on copies of q
-and k, then rth_attn_decode_append_split on the rotated rows): cache bytes,
-scales and outputs bit-identical, q and k_new left unrotated. Against the
+and k, then rth_attn_decode_append_split on the rotated rows): cache bytes and
+scales bit-identical, q and k_new left unrotated, outputs bit-identical at
+head_dim 256 and within half the oracle bounds below it (the plain fused kernel attends
+to the appended key before its cache tiles, these kernels after them). Against the
 oracle: the rotated rows equal O.rope_apply_bf16 bit for bit, the new cache
 row equals the oracle's quantizer on them, and the output is within max-abs
 2e-2 / mean-abs 2e-3 of the oracle's attention."""
@@ -23,6 +25,21 @@ from test_gpu_paged import gather, make_pair
 pytestmark = pytest.mark.gpu
 
 MAX_ABS, MEAN_ABS = 2e-2, 2e-3
+
+
+def assert_same_up_to_key_order(got, ref, d):
+    """The plain fused append + decode (head_dim <= 128) attends to the
+    appended key before its cache tiles, the RoPE / q-k-norm kernels after
+    them: the same terms, but the lazy softmax reference then differs, and P
+    enters the value MFMAs as bf16 (2^-9 relative per term) against another
+    reference, while the row sum takes the fp32 p. Bit-identical at head_dim
+    256 (both after); otherwise within max-abs 1e-2 / mean-abs 1e-3, half
+    the oracle bounds (each output is also checked against the oracle)."""
+    if d > 128:
+        assert np.array_equal(got, ref)
+        return
+    mx, mean = O.bf16_err(got, O.bf16_to_f32(ref))
+    assert mx <= 1e-2 and mean <= 1e-3, (mx, mean)
 
 
 def inv_table(d, kind):
@@ -81,7 +98,7 @@ def test_rope_decode_step_equals_two_step(cache_len, hq, hkv, d, splits, kind, p
     for a, b in ((ks1, ks2), (vs1, vs2)):
         assert np.array_equal(a.cpu().numpy().view(np.uint32), b.cpu().numpy().view(np.uint32))
     got = bf16_host(out1)
-    assert np.array_equal(got, bf16_host(out2))
+    assert_same_up_to_key_order(got, bf16_host(out2), d)
 
     q_rot = O.rope_apply_bf16(q[None], np.array([pos], np.int32), inv)[0]
     k_rot = O.rope_apply_bf16(kn[None], np.array([pos], np.int32), inv)[0]
@@ -203,7 +220,7 @@ def test_qk_norm_rope_decode_step_equals_unfused(cache_len, hq, hkv, d, splits, 
     for a, b in ((ks1, ks2), (vs1, vs2)):
         assert np.array_equal(a.cpu().numpy().view(np.uint32), b.cpu().numpy().view(np.uint32))
     got = bf16_host(out1)
-    assert np.array_equal(got, bf16_host(out2))
+    assert_same_up_to_key_order(got, bf16_host(out2), d)
 
     lanes = R.rmsnorm_lanes(d)
     q_t = O.rope_apply_bf16(O.rmsnorm_bf16(q, qg, eps, lanes)[None], np.array([pos], np.int32),
