@@ -313,6 +313,20 @@ __host__ __device__ constexpr int dec_q_blocks(int hq, int hkv, int head_dim) {
     return 0;
 }
 
+// Whether a solo launch may put all units of each kv head on one XCD
+// (workgroup bid runs on XCD bid % 8) and the merge workgroups of its q heads
+// on the same XCD: a kernel reads what the previous kernel wrote on its own
+// XCD from L2, from another XCD only after a much longer trip (measured: a
+// 3 MB exchange 0.9 us same-XCD against 3.0 us cross-XCD). Both kernels take
+// this mapping only when every live split holds one tile (tiles < 2 * splits,
+// decided on device from *cache_len): with more tiles the kernel streams, and
+// every XCD fetching all the interleaved [token, kv_head] scale lines for the
+// 4 bytes of its kv head costs more than the merge saves (131072 keys: 48 ->
+// 61 us per call).
+__host__ __device__ constexpr bool dec_xcd_local(int hkv, int num_splits) {
+    return (hkv & 7) == 0 && (num_splits & 7) == 0;
+}
+
 __host__ __device__ constexpr int dec_workgroups(int num_splits, int hkv, int kvg) {
     return (kvg > 0) ? num_splits * (hkv / kvg)
                      : (num_splits * hkv + kDecWaves - 1) / kDecWaves;
@@ -623,10 +637,26 @@ __device__ __forceinline__ void decode_body(
     // coop: workgroup = (group of gkv kv heads, split); wave w serves kv head
     //       w % gkv of the group and share j = w / gkv of its tiles
     // solo: wave = (kv head, split) unit; adjacent units are the kv heads of
-    //       one split, so a workgroup's waves share the scale lines in L1.
+    //       one split, so a workgroup's waves share the scale lines in L1,
+    //       except with one tile per split on XCD-local shapes (below).
     int       kvh, si;
     const int wpk = kDecWaves / pt.gkv;   // coop: waves per kv head
-    if (!pt.coop) {
+    if (!pt.coop && pt.base <= 1 && dec_xcd_local(hkv, num_splits)) {
+        // Workgroup = 8 consecutive splits of one kv head, on XCD kvh % 8
+        // (dec_xcd_local).
+        const int r  = bid >> 3;
+        const int hh = hkv >> 3;   // kv heads per XCD
+        int       kh, sg;
+        if ((hh & (hh - 1)) == 0) {
+            kh = r & (hh - 1);
+            sg = r >> __builtin_ctz(hh);
+        } else {
+            kh = r % hh;
+            sg = r / hh;
+        }
+        kvh = kh * 8 + (bid & 7);
+        si  = sg * kDecWaves + wave;
+    } else if (!pt.coop) {
         const int unit = bid * kDecWaves + wave;
         // hkv is a power of two in every common shape: shifts, not divisions.
         if ((hkv & (hkv - 1)) == 0) {
@@ -1236,13 +1266,15 @@ __device__ __forceinline__ float quad_group_sum(float v) {
 // quad qd) sums 2^(m_s - M) l_s and 2^(m_s - M) acc_s for splits grp,
 // grp + kGroups, ... and d = 4qd .. 4qd+3 of the slice (weights <= 1, eight
 // loads in flight), and the sums add up by lane exchanges and one LDS step.
-// The first loads are issued before the split count is known (slot indices
-// clamped into the scratch), so they share one round trip with the read of
-// *cache_len; slots no split wrote in this call are dropped by a select.
+// The head a workgroup merges depends on *cache_len where the split kernel
+// may have run XCD-local, so the loads follow that read; slot indices are
+// clamped into the scratch and slots no split wrote in this call are dropped
+// by a select. (Issuing the first loads of both candidate heads before the
+// read, to overlap it, cost 0.5-1.2 us per call.)
 template <int D>
 __global__ __launch_bounds__(kCombineThreads) void flash_decode_combine_kernel(
     uint16_t* __restrict__ out, const float* __restrict__ partial, int num_splits,
-    const int* __restrict__ cache_len, int hq, int kvg) {
+    const int* __restrict__ cache_len, int hq, int kvg, int xl_g) {
     constexpr int kQuads  = kCombineSlice / 4;
     constexpr int kGroups = kCombineThreads / kQuads;
     constexpr int kCWaves = kCombineThreads / kWave;
@@ -1250,8 +1282,24 @@ __global__ __launch_bounds__(kCombineThreads) void flash_decode_combine_kernel(
     __shared__ __attribute__((aligned(16))) f32x4 sm_acc[kCWaves][kQuads];
     __shared__ float sm_ll[kCWaves];
 
-    const int qh   = static_cast<int>(blockIdx.x);
-    const int dsl  = static_cast<int>(blockIdx.y) * kCombineSlice;
+    // xl_g > 0 (xl_g q heads per kv head) and one tile per split: the split
+    // kernel ran XCD-local (dec_xcd_local), and workgroup L (on XCD L % 8)
+    // takes a (q head, slice) of a kv head whose partials that XCD wrote.
+    const int n_keys = *cache_len + 1;
+    const DecPartition pt = dec_partition(n_keys, num_splits, kvg);
+    const int n_eff  = pt.n_eff;
+    int qh, dsl;
+    if (xl_g > 0 && pt.base <= 1) {
+        constexpr int kSlices = D / kCombineSlice;
+        const int     L       = static_cast<int>(blockIdx.x + blockIdx.y * gridDim.x);
+        const int     m       = L >> 3;
+        const int     t       = m / kSlices;
+        qh  = ((t / xl_g) * 8 + (L & 7)) * xl_g + t % xl_g;
+        dsl = (m % kSlices) * kCombineSlice;
+    } else {
+        qh  = static_cast<int>(blockIdx.x);
+        dsl = static_cast<int>(blockIdx.y) * kCombineSlice;
+    }
     const int tid  = static_cast<int>(threadIdx.x);
     const int grp  = tid / kQuads;
     const int qd   = tid - grp * kQuads;
@@ -1282,8 +1330,6 @@ __global__ __launch_bounds__(kCombineThreads) void flash_decode_combine_kernel(
     for (int e = 0; e < 4; ++e) {
         mr[e] = part_m[min(lane + kWave * e, num_splits - 1)];
     }
-    const int n_keys = *cache_len + 1;
-    const int n_eff  = dec_partition(n_keys, num_splits, kvg).n_eff;
     float     M      = -INFINITY;
     for (int s0 = 0;; s0 += 4 * kWave) {
 #pragma unroll
@@ -1607,7 +1653,7 @@ hipError_t launch_decode_valu(uint16_t* out, const uint16_t* q, const uint8_t* k
     hipLaunchKernelGGL(flash_decode_combine_kernel<D>,
                        dim3(static_cast<unsigned>(hq), static_cast<unsigned>(D / kCombineSlice)),
                        dim3(kCombineThreads), 0, stream, out, partial, num_splits, cache_len,
-                       hq, 0);
+                       hq, 0, 0);
     return hipGetLastError();
 }
 
@@ -1675,7 +1721,8 @@ hipError_t launch_decode(uint16_t* out, const uint16_t* q, const uint8_t* k,
     hipLaunchKernelGGL(flash_decode_combine_kernel<D>,
                        dim3(static_cast<unsigned>(hq), static_cast<unsigned>(D / kCombineSlice)),
                        dim3(kCombineThreads), 0, stream, out, partial, num_splits,
-                       cache_len, hq, kvg);
+                       cache_len, hq, kvg,
+                       (kvg == 0 && dec_xcd_local(hkv_v, num_splits)) ? hq / hkv_v : 0);
     return hipGetLastError();
 }
 

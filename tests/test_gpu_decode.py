@@ -266,6 +266,31 @@ def test_score_dynamic_range(splits):
     check(got, q, k8, v8, ks, vs, total - 1, hq, hkv, d, scale)
 
 
+@pytest.mark.parametrize("hq,hkv,splits", [(24, 8, 32), (32, 16, 32), (64, 2, 16), (16, 4, 32)])
+def test_xcd_local_mapping_switch(hq, hkv, splits):
+    """With 8k (virtual) kv heads and 8k splits, the split and merge kernels
+    put each kv head's units on one XCD while every live split holds one
+    32-key tile (tiles < 2 * splits) and use the split-major mapping beyond;
+    both kernels decide from *cache_len. Depths on either side of the switch,
+    in both orders on one scratch, match the oracle (64Q/2KV runs as 8
+    virtual kv heads; 16Q/4KV never switches)."""
+    d = 128
+    scale = np.float32(1.0 / np.sqrt(d))
+    edge = 2 * splits * 32
+    total = edge + 40
+    q = O.normal_bf16((hq, d), 71)
+    _, _, k8, v8, ks, vs = make_cache(total, hkv, d, kind="normal", seed=hq + hkv)
+    partial = R.new_flash_split_scratch(hq, d, splits)
+    k8d, v8d, ksd, vsd, qd = u8_dev(k8), u8_dev(v8), f32_dev(ks), f32_dev(vs), bf16_dev(q)
+    for ctx in (edge + 33, edge - 32, edge, edge - 31, edge + 1, splits * 32 - 5):
+        step(f"decode xcd switch hq={hq} hkv={hkv} splits={splits} ctx={ctx}")
+        out = torch.empty((hq, d), dtype=torch.bfloat16, device=DEV)
+        R.flash_decode_split_bf16(out, qd, k8d, v8d, ksd, vsd, partial, splits,
+                                  int_dev(ctx - 1), hq, hkv, d, scale)
+        sync()
+        check(bf16_host(out), q, k8, v8, ks, vs, ctx - 1, hq, hkv, d, scale)
+
+
 @pytest.mark.parametrize("cache_len,hq,hkv,d,splits", [
     (0, 24, 8, 128, None), (1, 24, 8, 128, None), (31, 24, 8, 128, None), (32, 24, 8, 128, None),
     (2040, 24, 8, 128, None), (8195, 24, 8, 128, None), (9000, 32, 8, 128, 64),
