@@ -24,16 +24,17 @@
 //  * Partitions (see DecPartition):
 //      - num_splits * Hkv >= 8 * CUs units: one WAVE per (kv head, split)
 //        unit. A workgroup holds the kv heads of one split (its waves share
-//        the interleaved scale lines in L1); waves never wait for each
-//        other and each writes its own partial.
+//        the interleaved scale lines in L1), or, when every split holds one
+//        tile, consecutive splits of one kv head on one XCD (so the merge
+//        reads that XCD's L2); waves never wait for each other and each
+//        writes its own partial.
 //      - fewer units (e.g. 64 splits x 8 kv heads): one workgroup per
 //        (group of kv heads, split), sized so the grid fills the chip; the
-//        waves of one kv head take contiguous shares of the split's tiles
+//        waves of one kv head take every (8 / kvg)-th tile of the split
 //        and merge in LDS. Workgroups of one split land on one XCD.
 //  * A second small kernel merges the splits of every (q head, 16-wide d
-//    slice): one round of loads issued before *cache_len is known, an
-//    online max per thread over a strided subset of splits, lane exchanges,
-//    one LDS step. The scratch layout is the reference's ([Hq,S] m, [Hq,S]
+//    slice): the head maximum from the m row, then weighted sums over a
+//    strided subset of splits per thread, lane exchanges, one LDS step. The scratch layout is the reference's ([Hq,S] m, [Hq,S]
 //    l, [Hq,S,D] acc); it needs no initialization.
 //
 // Split si holds an even share of the kTileKeys-key tiles over the keys; the
@@ -239,8 +240,9 @@ __device__ __forceinline__ void k_rows_to_mfma(TileRaw<D>& t, uint8_t* buf, int 
 // Partition of the decode work for one call. With fewer units than one
 // round of wave slots (num_splits * hkv < 8 * CUs) the host launches one
 // workgroup per (group of kvg kv heads, split): the workgroup's waves are kvg kv heads x
-// 8 / kvg waves per kv head, the waves of one kv head take contiguous shares
-// of the split's tiles and merge in LDS ("coop"); kvg is chosen so the grid still fills
+// 8 / kvg waves per kv head, the waves of one kv head take interleaved shares
+// of the split's tiles (every (8 / kvg)-th tile; contiguous shares measured
+// 128K at 64 splits 53.4 vs 52.0 us) and merge in LDS ("coop"); kvg is chosen so the grid still fills
 // the chip (more kv heads per workgroup read longer runs of each interleaved
 // [token, kv_head] row). Otherwise (kvg = 0, and always in the VALU kernel)
 // it launches one wave per (kv head, split) unit, eight per workgroup, with
@@ -759,13 +761,14 @@ __device__ __forceinline__ void decode_body(
     const bool virt    = owner && (!pt.coop || wave >= kDecWaves - pt.gkv);
     const int  k1      = owner ? p_new : min(split_tile(pt, si + 1) * kTileKeys, n_keys);
     const int  n_tiles = (k1 - k0 + kTileKeys - 1) / kTileKeys;
-    // Tiles [t_first, last_tile] of the split: all of them for a solo wave;
-    // in coop mode wave j of its kv head's wpk waves takes a contiguous
-    // share (floor(j n / wpk) .. floor((j + 1) n / wpk) - 1).
+    // The wave's cnt tiles of the split, tile_at(0 .. cnt - 1): all of them
+    // for a solo wave; in coop mode wave j of its kv head's wpk waves takes
+    // tiles j, j + wpk, j + 2 wpk, ..., so the waves of a kv head read
+    // neighbouring tiles at the same time.
     const int  wj        = pt.coop ? wave / pt.gkv : 0;
     const int  wn        = pt.coop ? wpk : 1;
-    const int  t_first   = pt.coop ? (wj * n_tiles) / wn : 0;
-    const int  last_tile = pt.coop ? ((wj + 1) * n_tiles) / wn - 1 : n_tiles - 1;
+    const int  cnt       = pt.coop ? (n_tiles - wj + wn - 1) / wn : n_tiles;
+    auto       tile_at   = [&](int i) { return pt.coop ? wj + i * wn : i; };
 
     // Q^T as the B operand: column n = q head n of the group. Columns past
     // G repeat head 0: their scores only ever mirror head 0's (so they never
@@ -1006,7 +1009,7 @@ __device__ __forceinline__ void decode_body(
     }
     };
     constexpr int kRing     = DecTraits<D>::kRing;
-    if (t_first <= last_tile) {
+    if (cnt > 0) {
         auto tile_delta = [&](int kb) {
             if constexpr (kPaged) {
                 return paged_row(kb, block_table, block_shift) - kb;
@@ -1024,25 +1027,25 @@ __device__ __forceinline__ void decode_body(
             TileRaw<D> ring[kRing];
 #pragma unroll
             for (int r = 0; r + 1 < kRing; ++r) {
-                load(ring[r], k0 + min(t_first + r, last_tile) * kTileKeys);
+                load(ring[r], k0 + tile_at(min(r, cnt - 1)) * kTileKeys);
             }
             rope_q();   // behind the first tile loads
             if constexpr (kEarlyKey) {
                 new_key();
             }
-            for (int t = t_first;; t += kRing) {
+            for (int t = 0;; t += kRing) {
                 bool done = false;
 #pragma unroll
                 for (int r = 0; r < kRing; ++r) {
                     if (!done) {
                         const int tr  = t + r;
-                        const int kbn = k0 + min(tr + kRing - 1, last_tile) * kTileKeys;
-                        if (kPaged || tr + kRing - 1 <= last_tile) {
+                        const int kbn = k0 + tile_at(min(tr + kRing - 1, cnt - 1)) * kTileKeys;
+                        if (kPaged || tr + kRing - 1 <= cnt - 1) {
                             load(ring[(r + kRing - 1) % kRing], kbn);
                         }
                         k_rows_to_mfma<D>(ring[r], kbuf, lane);
-                        process(ring[r], k0 + tr * kTileKeys, k1);
-                        done = tr + 1 > last_tile;
+                        process(ring[r], k0 + tile_at(tr) * kTileKeys, k1);
+                        done = tr + 1 > cnt - 1;
                     }
                 }
                 if (done) {
@@ -1057,7 +1060,7 @@ __device__ __forceinline__ void decode_body(
         // nontemporal loads, 32K at 256 splits (4 tiles per wave) 20.5 ->
         // 19.5 us; 8K at 256 splits and 128K at 64 one-kv-head cooperative
         // splits 6-8 % slower with them).
-        if ((!pt.coop || pt.gkv > 1) && last_tile - t_first >= kNtMinTiles) {
+        if ((!pt.coop || pt.gkv > 1) && cnt - 1 >= kNtMinTiles) {
             stream.template operator()<true>();
         } else {
             stream.template operator()<false>();
