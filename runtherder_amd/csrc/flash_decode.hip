@@ -319,12 +319,13 @@ __host__ __device__ constexpr int dec_q_blocks(int hq, int hkv, int head_dim) {
 // (workgroup bid runs on XCD bid % 8) and the merge workgroups of its q heads
 // on the same XCD: a kernel reads what the previous kernel wrote on its own
 // XCD from L2, from another XCD only after a much longer trip (measured: a
-// 3 MB exchange 0.9 us same-XCD against 3.0 us cross-XCD). Both kernels take
-// this mapping only when every live split holds one tile (tiles < 2 * splits,
-// decided on device from *cache_len): with more tiles the kernel streams, and
-// every XCD fetching all the interleaved [token, kv_head] scale lines for the
-// 4 bytes of its kv head costs more than the merge saves (131072 keys: 48 ->
-// 61 us per call).
+// 3 MB exchange 0.9 us same-XCD against 3.0 us cross-XCD). The split kernel
+// takes this mapping only when every live split holds one tile (tiles < 2 *
+// splits, decided on device from *cache_len): with more tiles the kernel
+// streams, and every XCD fetching all the interleaved [token, kv_head] scale
+// lines for the 4 bytes of its kv head costs more than the merge saves
+// (131072 keys: 48 -> 61 us per call). The merge takes it on every call of
+// such a shape.
 __host__ __device__ constexpr bool dec_xcd_local(int hkv, int num_splits) {
     return (hkv & 7) == 0 && (num_splits & 7) == 0;
 }
@@ -1269,11 +1270,9 @@ __device__ __forceinline__ float quad_group_sum(float v) {
 // quad qd) sums 2^(m_s - M) l_s and 2^(m_s - M) acc_s for splits grp,
 // grp + kGroups, ... and d = 4qd .. 4qd+3 of the slice (weights <= 1, eight
 // loads in flight), and the sums add up by lane exchanges and one LDS step.
-// The head a workgroup merges depends on *cache_len where the split kernel
-// may have run XCD-local, so the loads follow that read; slot indices are
-// clamped into the scratch and slots no split wrote in this call are dropped
-// by a select. (Issuing the first loads of both candidate heads before the
-// read, to overlap it, cost 0.5-1.2 us per call.)
+// The first loads are issued before the split count is known (slot indices
+// clamped into the scratch), so they share one round trip with the read of
+// *cache_len; slots no split wrote in this call are dropped by a select.
 template <int D>
 __global__ __launch_bounds__(kCombineThreads) void flash_decode_combine_kernel(
     uint16_t* __restrict__ out, const float* __restrict__ partial, int num_splits,
@@ -1285,14 +1284,14 @@ __global__ __launch_bounds__(kCombineThreads) void flash_decode_combine_kernel(
     __shared__ __attribute__((aligned(16))) f32x4 sm_acc[kCWaves][kQuads];
     __shared__ float sm_ll[kCWaves];
 
-    // xl_g > 0 (xl_g q heads per kv head) and one tile per split: the split
-    // kernel ran XCD-local (dec_xcd_local), and workgroup L (on XCD L % 8)
-    // takes a (q head, slice) of a kv head whose partials that XCD wrote.
-    const int n_keys = *cache_len + 1;
-    const DecPartition pt = dec_partition(n_keys, num_splits, kvg);
-    const int n_eff  = pt.n_eff;
+    // xl_g > 0 (an XCD-local shape, xl_g q heads per kv head): workgroup L
+    // (on XCD L % 8) takes a (q head, slice) of a kv head on that XCD. With
+    // one tile per split the split kernel wrote that kv head's partials on
+    // the same XCD (dec_xcd_local); otherwise they are spread over all XCDs
+    // whichever head a workgroup takes, so the assignment needs no
+    // *cache_len and the first loads go out before that read.
     int qh, dsl;
-    if (xl_g > 0 && pt.base <= 1) {
+    if (xl_g > 0) {
         constexpr int kSlices = D / kCombineSlice;
         const int     L       = static_cast<int>(blockIdx.x + blockIdx.y * gridDim.x);
         const int     m       = L >> 3;
@@ -1333,6 +1332,8 @@ __global__ __launch_bounds__(kCombineThreads) void flash_decode_combine_kernel(
     for (int e = 0; e < 4; ++e) {
         mr[e] = part_m[min(lane + kWave * e, num_splits - 1)];
     }
+    const int n_keys = *cache_len + 1;
+    const int n_eff  = dec_partition(n_keys, num_splits, kvg).n_eff;
     float     M      = -INFINITY;
     for (int s0 = 0;; s0 += 4 * kWave) {
 #pragma unroll
