@@ -229,8 +229,8 @@ int rth_attn_decode_append_split_paged(uint16_t* out, const uint16_t* q, uint8_t
  * unrotated) are read only: both are rotated in registers by the angles of
  * positions[0] with rth_rope_bf16's arithmetic, so the cache row written at
  * *cache_len is byte-identical to rth_rope_bf16 + rth_kv_append_fp8 and the
- * output equals rth_attn_decode_append_split on the rotated q and k (the
- * same terms, the appended key summed in another order). Shapes
+ * output is bit-identical to rth_attn_decode_append_split on the rotated q
+ * and k. Shapes
  * rth_decode_path reports as RTH_DECODE_MFMA under the automatic choice
  * (head_dim 64, 128, 256); others fail with an error. block_table == NULL (or the first entry point): the
  * contiguous layout. */
@@ -255,7 +255,7 @@ int rth_attn_decode_rope_append_split_paged(uint16_t* out, const uint16_t* q, ui
  * KVCache::append -> run (reference src/model/supported/llama/
  * qwen3.cu:189-202), in the two launches of rth_attn_decode_append_split.
  * q and k_new are read only; the cache row equals rth_qk_norm_rope_append_fp8's
- * byte for byte, and the output equals (up to summation order)
+ * byte for byte, and the output is bit-identical to
  * rth_attn_decode_append_split on q and
  * k_new after rth_rmsnorm_bf16 (per head) and rth_rope_bf16. Shapes as
  * rth_attn_decode_rope_append_split. */

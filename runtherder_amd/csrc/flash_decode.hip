@@ -990,10 +990,10 @@ __device__ __forceinline__ void decode_body(
     // 13.2 us with it vs 15.1 without, 128K 50.4 vs 51.3, 2K 9.6 vs 9.3).
     // The appended key (owner waves): quantized, stored and attended to.
     // kEarlyKey: right behind the first tile's loads, so that the work
-    // overlaps their latency instead of trailing the stream (the RoPE /
-    // q-k-norm kernels and head_dim 256 do it after the stream: earlier, they
-    // spill).
-    constexpr bool kEarlyKey = kAppend && !kRope && D <= 128;
+    // overlaps their latency instead of trailing the stream (in the RoPE /
+    // q-k-norm kernels after the rotation table's barrier; head_dim 256 does
+    // it after the stream: earlier, it spills).
+    constexpr bool kEarlyKey = kAppend && D <= 128;
     auto new_key = [&]() __attribute__((always_inline)) {
     if (kAppend && virt) {
         TileRaw<D>    vt;
