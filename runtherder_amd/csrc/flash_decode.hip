@@ -458,7 +458,8 @@ __device__ __forceinline__ void quantize_new_token(TileRaw<D>& vt, const uint16_
                                                    const float* rs = nullptr,
                                                    const uint16_t* k_norm = nullptr,
                                                    float eps = 0.0f, const u32x4* pk = nullptr,
-                                                   const uint32_t* pv = nullptr) {
+                                                   const uint32_t* pv = nullptr,
+                                                   const u32x4* pr = nullptr) {
     using T     = DecTraits<D>;
     const int n = lane & 15;
     const int g = lane >> 4;
@@ -469,9 +470,21 @@ __device__ __forceinline__ void quantize_new_token(TileRaw<D>& vt, const uint16_
     for (int c = 0; c < T::kKChunks; ++c) {
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
-            kw[c][h] = (n == 0) ? (pk != nullptr ? pk[2 * c + h]
-                                                 : *reinterpret_cast<const u32x4*>(kx + 16 * g + 64 * c + 8 * h))
-                                : u32x4{0u, 0u, 0u, 0u};
+            if (pr != nullptr) {
+                // Element 16g + 64c + 8h of the row sits in lane 2g + 8c + h
+                // of the preloaded rmsnorm_vec layout.
+                const int src = 4 * (2 * g + 8 * c + h);
+                u32x4     w;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    w[e] = static_cast<uint32_t>(__builtin_amdgcn_ds_bpermute(src, static_cast<int>((*pr)[e])));
+                }
+                kw[c][h] = (n == 0) ? w : u32x4{0u, 0u, 0u, 0u};
+            } else {
+                kw[c][h] = (n == 0) ? (pk != nullptr ? pk[2 * c + h]
+                                                     : *reinterpret_cast<const u32x4*>(kx + 16 * g + 64 * c + 8 * h))
+                                    : u32x4{0u, 0u, 0u, 0u};
+            }
         }
     }
     if (k_norm != nullptr) {
@@ -480,7 +493,7 @@ __device__ __forceinline__ void quantize_new_token(TileRaw<D>& vt, const uint16_
         constexpr int kL = D / 8;
         u32x4 rv = {0u, 0u, 0u, 0u};
         if (lane < kL) {
-            rv = *reinterpret_cast<const u32x4*>(kx + 8 * lane);
+            rv = (pr != nullptr) ? *pr : *reinterpret_cast<const u32x4*>(kx + 8 * lane);
         }
         const float rrms = __builtin_bit_cast(
             float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(
@@ -735,17 +748,26 @@ __device__ __forceinline__ void decode_body(
     // The appended row's bf16 words, issued before the stream (D <= 128: the
     // 40 VGPRs they hold through the stream spill the D = 256 kernels). Plain
     // loads, not loads inside the owner branch: a branch-merged load makes the
-    // compiler wait for every outstanding load at the merge.
+    // compiler wait for every outstanding load at the merge. The q/k-norm
+    // kernels hold the K row once, in rmsnorm_vec's layout (16 bytes on each
+    // of lanes 0 .. D/8-1), and gather the tile layout from it with lane
+    // permutes (both layouts held through the stream spill there; per call
+    // at 8K the preload saves ~1 us of the owner wave's round trip).
     [[maybe_unused]] u32x4    pre_k[DecTraits<D>::kKChunks * 2];
     [[maybe_unused]] uint32_t pre_v[DecTraits<D>::kVBytes / 2];
-    if constexpr (kAppend && !kNorm && D <= 128) {
+    [[maybe_unused]] u32x4    pre_r = {0u, 0u, 0u, 0u};   // kNorm: the row in rmsnorm_vec's layout
+    if constexpr (kAppend && D <= 128) {
         const uint16_t* kx = k_new + static_cast<int64_t>(kvc) * D;
         const uint16_t* vx = v_new + static_cast<int64_t>(kvc) * D;
+        if constexpr (kNorm) {
+            pre_r = *reinterpret_cast<const u32x4*>(kx + 8 * (lane & (D / 8 - 1)));
+        } else {
 #pragma unroll
-        for (int c = 0; c < DecTraits<D>::kKChunks; ++c) {
+            for (int c = 0; c < DecTraits<D>::kKChunks; ++c) {
 #pragma unroll
-            for (int h = 0; h < 2; ++h) {
-                pre_k[2 * c + h] = *reinterpret_cast<const u32x4*>(kx + 16 * ((lane >> 4) & 3) + 64 * c + 8 * h);
+                for (int h = 0; h < 2; ++h) {
+                    pre_k[2 * c + h] = *reinterpret_cast<const u32x4*>(kx + 16 * ((lane >> 4) & 3) + 64 * c + 8 * h);
+                }
             }
         }
 #pragma unroll
@@ -1005,7 +1027,8 @@ __device__ __forceinline__ void decode_body(
                               kRope ? sm_rope : nullptr, kRope ? sm_rope + D / 2 : nullptr,
                               kNorm ? sm_gain + kMaxD : nullptr, eps,
                               (kAppend && !kNorm && D <= 128) ? pre_k : nullptr,
-                              (kAppend && !kNorm && D <= 128) ? pre_v : nullptr);
+                              (kAppend && D <= 128) ? pre_v : nullptr,
+                              (kAppend && kNorm && D <= 128) ? &pre_r : nullptr);
         process(vt, p_new, p_new + 1);
     }
     };
