@@ -635,10 +635,10 @@ __device__ __forceinline__ void decode_body(
     __shared__ float sm_m[kDecWaves][16];
     __shared__ float sm_l[kDecWaves][16];
     // kRope: cos (first D/2) and sin (next D/2) of the RoPE angles, built by
-    // wave 0 for the whole workgroup.
-    __shared__ __attribute__((aligned(16))) float sm_rope[kMaxD];
-    // kNorm: the q_norm (first kMaxD) and k_norm gains, staged by wave 0.
-    __shared__ __attribute__((aligned(16))) uint16_t sm_gain[2 * kMaxD];
+    // every wave for itself (no workgroup barrier).
+    __shared__ __attribute__((aligned(16))) float sm_rope_w[kRope ? kDecWaves : 1][kRope ? D : 1];
+    // kNorm: the q_norm (first D) and k_norm gains, staged by every wave.
+    __shared__ __attribute__((aligned(16))) uint16_t sm_gain_w[kNorm ? kDecWaves : 1][kNorm ? 2 * D : 1];
 
     const int G    = hq / hkv;
     const int tid  = static_cast<int>(threadIdx.x);
@@ -699,9 +699,10 @@ __device__ __forceinline__ void decode_body(
         kvh = grp * pt.gkv + wave % pt.gkv;
     }
     // kRope: the angle inputs are loaded here, ahead of every tile load, so
-    // building the table later waits for nothing else in flight; every wave
-    // passes exactly one workgroup barrier, the one after which wave 0's
-    // table is complete (a wave without keys passes it here).
+    // building the table later waits for nothing else in flight. Each wave
+    // builds its own table behind its first tile loads, where the double
+    // sincos hides under their latency (one table per workgroup behind a
+    // workgroup barrier measured 0.4-1.2 us slower per call).
     [[maybe_unused]] float    rope_inv[kRopeIter] = {};
     [[maybe_unused]] int      rope_pos            = 0;
     [[maybe_unused]] uint32_t gain_q[kRopeIter]   = {};   // 2 bf16 per lane and step
@@ -719,26 +720,23 @@ __device__ __forceinline__ void decode_body(
             }
         }
     }
+    float*    sm_rope = sm_rope_w[kRope ? wave : 0];
+    uint16_t* sm_gain = sm_gain_w[kNorm ? wave : 0];
     auto rope_sync = [&]() {
         if constexpr (kRope) {
-            if (wave == 0) {
-                if constexpr (kNorm) {
+            if constexpr (kNorm) {
 #pragma unroll
-                    for (int j = 0; j < kRopeIter; ++j) {
-                        if (lane + j * kWave < D / 2) {
-                            reinterpret_cast<uint32_t*>(sm_gain)[lane + j * kWave] = gain_q[j];
-                            reinterpret_cast<uint32_t*>(sm_gain + kMaxD)[lane + j * kWave] =
-                                gain_k[j];
-                        }
+                for (int j = 0; j < kRopeIter; ++j) {
+                    if (lane + j * kWave < D / 2) {
+                        reinterpret_cast<uint32_t*>(sm_gain)[lane + j * kWave] = gain_q[j];
+                        reinterpret_cast<uint32_t*>(sm_gain + D)[lane + j * kWave] = gain_k[j];
                     }
                 }
-                rope_table_wave<D>(sm_rope, sm_rope + D / 2, rope_pos, rope_inv, lane);
             }
-            __syncthreads();
+            rope_table_wave<D>(sm_rope, sm_rope + D / 2, rope_pos, rope_inv, lane);
         }
     };
     if (si >= pt.n_eff) {   // uniform per workgroup in coop mode
-        rope_sync();
         return;
     }
     // Wave-uniform by construction; kept in scalar registers so that tile
@@ -1025,7 +1023,7 @@ __device__ __forceinline__ void decode_body(
                               v_new + static_cast<int64_t>(kvc) * D, k_w + row * D,
                               v_w + row * D, ks_w + row, vs_w + row, lane, kvh == kvc * nqb,
                               kRope ? sm_rope : nullptr, kRope ? sm_rope + D / 2 : nullptr,
-                              kNorm ? sm_gain + kMaxD : nullptr, eps,
+                              kNorm ? sm_gain + D : nullptr, eps,
                               (kAppend && !kNorm && D <= 128) ? pre_k : nullptr,
                               (kAppend && D <= 128) ? pre_v : nullptr,
                               (kAppend && kNorm && D <= 128) ? &pre_r : nullptr);
