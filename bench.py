@@ -26,6 +26,7 @@ from __future__ import annotations
 import argparse
 import json
 import math
+import statistics
 import os
 import sys
 import time
@@ -72,12 +73,14 @@ class EventTimer:
         self.ms = self.a.elapsed_time(self.b)
 
 
-def graph_us(torch, stream, fn, iters):
+def graph_us(torch, stream, fn, iters, replays=5):
     """Microseconds per call of fn, captured iters times in one HIP graph and
-    timed over a replay (one warm replay first): the kernels back to back,
-    without the host launch rate of an eager loop."""
+    timed over `replays` replays (one warm replay first), median of them: the
+    kernels back to back, without the host launch rate of an eager loop, and
+    one disturbed replay does not move the figure."""
     g = torch.cuda.CUDAGraph()
     torch.cuda.synchronize()   # work queued on other streams lands first
+    times = []
     with torch.cuda.stream(stream):
         fn()
         torch.cuda.synchronize()
@@ -85,10 +88,12 @@ def graph_us(torch, stream, fn, iters):
             for _ in range(iters):
                 fn()
         g.replay()
-        with EventTimer(torch, stream) as t:
-            g.replay()
+        for _ in range(replays):
+            with EventTimer(torch, stream) as t:
+                g.replay()
+            times.append(t.ms)
     torch.cuda.synchronize()
-    return t.ms * 1e3 / iters
+    return statistics.median(times) * 1e3 / iters
 
 
 def bench_decode(torch, R, args, stream):
