@@ -649,7 +649,28 @@ __device__ __forceinline__ void decode_body(
     const int bid  = static_cast<int>(blockIdx.x);
 
     const int          n_keys = *cache_len + 1;
-    const DecPartition pt     = dec_partition(n_keys, num_splits, kvg);
+    DecPartition pt = dec_partition(n_keys, num_splits, kvg);
+    // Append calls on a solo launch whose cache keys leave a split free: the
+    // appended key gets a split of its own (slot owner_si), so its wave
+    // attends to it alone instead of behind a cache tile (at short contexts
+    // that wave finished last: 2041 keys 8.8 -> 7.4 us per call); the cache
+    // tiles go one per split. The merge derives the same slot count. (Kept
+    // out of dec_partition, and marked unlikely: otherwise the prologue of
+    // every kernel is scheduled around it, 0.1-0.2 us per call at 8K.)
+    int owner_si = pt.n_eff - 1;
+    int n_live   = pt.n_eff;
+    int key_end  = n_keys;   // cache keys a non-owner split may read
+    if constexpr (kAppend) {
+        const int cache_tiles = (n_keys - 1 + kTileKeys - 1) / kTileKeys;
+        if (__builtin_expect(!pt.coop && cache_tiles < num_splits, 0)) {
+            pt.n_eff = cache_tiles;
+            pt.base  = 1;
+            pt.rem   = 0;
+            owner_si = cache_tiles;
+            n_live   = cache_tiles + 1;
+            key_end  = n_keys - 1;
+        }
+    }
     // coop: workgroup = (group of gkv kv heads, split); wave w serves kv head
     //       w % gkv of the group and share j = w / gkv of its tiles
     // solo: wave = (kv head, split) unit; adjacent units are the kv heads of
@@ -736,7 +757,7 @@ __device__ __forceinline__ void decode_body(
             rope_table_wave<D>(sm_rope, sm_rope + D / 2, rope_pos, rope_inv, lane);
         }
     };
-    if (si >= pt.n_eff) {   // uniform per workgroup in coop mode
+    if (si >= n_live) {   // uniform per workgroup in coop mode
         return;
     }
     // Wave-uniform by construction; kept in scalar registers so that tile
@@ -778,9 +799,9 @@ __device__ __forceinline__ void decode_body(
     // only the keys before it from the cache; one of its waves adds the new
     // key from registers.
     const int  p_new   = n_keys - 1;
-    const bool owner   = kAppend && (si == pt.n_eff - 1);
+    const bool owner   = kAppend && (si == owner_si);
     const bool virt    = owner && (!pt.coop || wave >= kDecWaves - pt.gkv);
-    const int  k1      = owner ? p_new : min(split_tile(pt, si + 1) * kTileKeys, n_keys);
+    const int  k1      = owner ? p_new : min(split_tile(pt, si + 1) * kTileKeys, key_end);
     const int  n_tiles = (k1 - k0 + kTileKeys - 1) / kTileKeys;
     // The wave's cnt tiles of the split, tile_at(0 .. cnt - 1): all of them
     // for a solo wave; in coop mode wave j of its kv head's wpk waves takes
@@ -1297,7 +1318,7 @@ __device__ __forceinline__ float quad_group_sum(float v) {
 template <int D>
 __global__ __launch_bounds__(kCombineThreads) void flash_decode_combine_kernel(
     uint16_t* __restrict__ out, const float* __restrict__ partial, int num_splits,
-    const int* __restrict__ cache_len, int hq, int kvg, int xl_g) {
+    const int* __restrict__ cache_len, int hq, int kvg, int xl_g, int append) {
     constexpr int kQuads  = kCombineSlice / 4;
     constexpr int kGroups = kCombineThreads / kQuads;
     constexpr int kCWaves = kCombineThreads / kWave;
@@ -1354,8 +1375,13 @@ __global__ __launch_bounds__(kCombineThreads) void flash_decode_combine_kernel(
         mr[e] = part_m[min(lane + kWave * e, num_splits - 1)];
     }
     const int n_keys = *cache_len + 1;
-    const int n_eff  = dec_partition(n_keys, num_splits, kvg).n_eff;
-    float     M      = -INFINITY;
+    // Live slots: as the split kernel derives them (an append call's key may
+    // hold a slot of its own).
+    const int cache_t = (n_keys + kTileKeys - 2) / kTileKeys;
+    const int n_eff   = (append != 0 && kvg == 0 && cache_t < num_splits)
+                            ? cache_t + 1
+                            : dec_partition(n_keys, num_splits, kvg).n_eff;
+    float     M       = -INFINITY;
     for (int s0 = 0;; s0 += 4 * kWave) {
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
@@ -1678,7 +1704,7 @@ hipError_t launch_decode_valu(uint16_t* out, const uint16_t* q, const uint8_t* k
     hipLaunchKernelGGL(flash_decode_combine_kernel<D>,
                        dim3(static_cast<unsigned>(hq), static_cast<unsigned>(D / kCombineSlice)),
                        dim3(kCombineThreads), 0, stream, out, partial, num_splits, cache_len,
-                       hq, 0, 0);
+                       hq, 0, 0, 0);
     return hipGetLastError();
 }
 
@@ -1747,7 +1773,8 @@ hipError_t launch_decode(uint16_t* out, const uint16_t* q, const uint8_t* k,
                        dim3(static_cast<unsigned>(hq), static_cast<unsigned>(D / kCombineSlice)),
                        dim3(kCombineThreads), 0, stream, out, partial, num_splits,
                        cache_len, hq, kvg,
-                       (kvg == 0 && dec_xcd_local(hkv_v, num_splits)) ? hq / hkv_v : 0);
+                       (kvg == 0 && dec_xcd_local(hkv_v, num_splits)) ? hq / hkv_v : 0,
+                       k_new != nullptr ? 1 : 0);
     return hipGetLastError();
 }
 
