@@ -650,24 +650,26 @@ __device__ __forceinline__ void decode_body(
 
     const int          n_keys = *cache_len + 1;
     DecPartition pt = dec_partition(n_keys, num_splits, kvg);
-    // Append calls on a solo launch whose cache keys leave a split free: the
-    // appended key gets a split of its own (slot owner_si), so its wave
-    // attends to it alone instead of behind a cache tile (at short contexts
-    // that wave finished last: 2041 keys 8.8 -> 7.4 us per call); the cache
-    // tiles go one per split. The merge derives the same slot count. (Kept
-    // out of dec_partition, and marked unlikely: otherwise the prologue of
-    // every kernel is scheduled around it, 0.1-0.2 us per call at 8K.)
+    // Append calls on a solo launch with at most two cache tiles per split
+    // when one split is kept back: the appended key gets that split of its
+    // own (slot owner_si), so its wave attends to it alone instead of behind
+    // a cache tile (that wave finished last: 2041 keys 8.8 -> 7.4 us per
+    // call, 8196 keys 10.97 -> 10.71); the cache tiles go one or two per
+    // split over the others. The merge derives the same slot count. (Kept out
+    // of dec_partition: otherwise the prologue of every kernel is scheduled
+    // around it, 0.1-0.2 us per call at 8K.)
     int owner_si = pt.n_eff - 1;
     int n_live   = pt.n_eff;
     int key_end  = n_keys;   // cache keys a non-owner split may read
     if constexpr (kAppend) {
         const int cache_tiles = (n_keys - 1 + kTileKeys - 1) / kTileKeys;
-        if (__builtin_expect(!pt.coop && cache_tiles < num_splits, 0)) {
-            pt.n_eff = cache_tiles;
-            pt.base  = 1;
-            pt.rem   = 0;
-            owner_si = cache_tiles;
-            n_live   = cache_tiles + 1;
+        if (__builtin_expect(!pt.coop && cache_tiles <= 2 * (num_splits - 1), 1)) {
+            const int n = min(num_splits - 1, cache_tiles);
+            pt.n_eff = n;
+            pt.base  = 1;                 // at most two cache tiles per split
+            pt.rem   = cache_tiles - n;
+            owner_si = n;
+            n_live   = n + 1;
             key_end  = n_keys - 1;
         }
     }
@@ -1378,8 +1380,8 @@ __global__ __launch_bounds__(kCombineThreads) void flash_decode_combine_kernel(
     // Live slots: as the split kernel derives them (an append call's key may
     // hold a slot of its own).
     const int cache_t = (n_keys + kTileKeys - 2) / kTileKeys;
-    const int n_eff   = (append != 0 && kvg == 0 && cache_t < num_splits)
-                            ? cache_t + 1
+    const int n_eff   = (append != 0 && kvg == 0 && cache_t <= 2 * (num_splits - 1))
+                            ? min(num_splits - 1, cache_t) + 1
                             : dec_partition(n_keys, num_splits, kvg).n_eff;
     float     M       = -INFINITY;
     for (int s0 = 0;; s0 += 4 * kWave) {

@@ -299,9 +299,11 @@ def test_xcd_local_mapping_switch(hq, hkv, splits):
     # q blocks: several units per cache head attend the new token, one stores it
     (700, 64, 2, 128, 16), (3000, 32, 1, 128, None), (130, 16, 1, 256, 8),
     # 256 splits: the appended key has a split of its own while the cache
-    # keys fill at most 255 tiles (cache_len <= 8160), then shares the last one
+    # keys fill at most 2 x 255 tiles (cache_len <= 16320), one or two per
+    # split, then shares the last split's tile
     (8159, 24, 8, 128, None), (8160, 24, 8, 128, None), (8161, 24, 8, 128, None),
-    (8191, 24, 8, 128, None), (8192, 24, 8, 128, None),
+    (8192, 24, 8, 128, None), (16319, 24, 8, 128, None), (16320, 24, 8, 128, None),
+    (16321, 24, 8, 128, None), (16352, 24, 8, 128, None),
 ])
 def test_decode_append_fused(cache_len, hq, hkv, d, splits):
     """Fused append + decode: the cache row equals the append kernel's bytes
