@@ -598,9 +598,10 @@ __device__ __forceinline__ void quantize_new_token(TileRaw<D>& vt, const uint16_
 }
 
 // kAppend: the call also appends one token (k_new, v_new [Hkv, D] bf16) at
-// row *cache_len of the cache; the unit whose split holds that key quantizes
-// it, stores codes and scales, and attends to it from registers, so no wave
-// reads the row being written.
+// row *cache_len of the cache; the owner unit (a split of its own when the
+// cache keys leave one, else the last split) quantizes it, stores codes and
+// scales, and attends to it from registers, so no wave reads the row being
+// written.
 // kPaged: K/V/scale rows are addressed through block_table (see paged_row).
 // nqb: q blocks per cache kv head. A group of more than 16 q heads (the
 // MFMA's 16 columns) is served as nqb virtual kv heads of G / nqb q heads
@@ -797,9 +798,8 @@ __device__ __forceinline__ void decode_body(
         }
     }
     const int k0 = split_tile(pt, si) * kTileKeys;
-    // With an append, the split holding the new key (the last one) reads
-    // only the keys before it from the cache; one of its waves adds the new
-    // key from registers.
+    // With an append, no split reads key p_new from the cache (it is being
+    // written); one wave of the owner split adds it from registers.
     const int  p_new   = n_keys - 1;
     const bool owner   = kAppend && (si == owner_si);
     const bool virt    = owner && (!pt.coop || wave >= kDecWaves - pt.gkv);
