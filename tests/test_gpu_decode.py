@@ -304,6 +304,11 @@ def test_xcd_local_mapping_switch(hq, hkv, splits):
     (8159, 24, 8, 128, None), (8160, 24, 8, 128, None), (8161, 24, 8, 128, None),
     (8192, 24, 8, 128, None), (16319, 24, 8, 128, None), (16320, 24, 8, 128, None),
     (16321, 24, 8, 128, None), (16352, 24, 8, 128, None),
+    # 64 kv heads x 32 splits (solo): the key's own split while the cache keys
+    # fit 2 x 31 tiles (cache_len <= 1984), one per split up to 31 tiles
+    (0, 64, 64, 128, 32), (31, 64, 64, 128, 32), (992, 64, 64, 128, 32),
+    (993, 64, 64, 128, 32), (1983, 64, 64, 128, 32), (1984, 64, 64, 128, 32),
+    (1985, 64, 64, 128, 32), (2100, 64, 64, 128, 32),
 ])
 def test_decode_append_fused(cache_len, hq, hkv, d, splits):
     """Fused append + decode: the cache row equals the append kernel's bytes
