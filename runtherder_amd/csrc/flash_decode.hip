@@ -1132,45 +1132,47 @@ __device__ __forceinline__ void decode_body(
     float*        part_o = partial + 2 * hs;
     if (pt.coop) {
         // Merge the waves of each kv head (waves kl, kl + gkv, ...): each
-        // scales its O^T by 2^(m_w - M) into its LDS rows, then the rows are
-        // summed along d.
+        // puts its m, l and unscaled O^T rows in LDS; after one barrier the
+        // threads sum the rows along d with the weights 2^(m_w - M), which
+        // each derives from the waves' m (a second barrier, with the waves
+        // scaling their own rows first, cost ~0.3 us per call).
         if (g == 0) {
             sm_m[wave][n] = m_run;
             sm_l[wave][n] = l_run;
         }
-        __syncthreads();
-        // Loops over the waves of one kv head run over all kDecWaves slots
-        // with a predicate, unrolled, so their LDS reads issue together.
-        const int kl = wave % pt.gkv;
         if (n < G) {
-            float M = -INFINITY;
-#pragma unroll
-            for (int j = 0; j < kDecWaves; ++j) {
-                if (j < wpk) {
-                    M = fmaxf(M, sm_m[kl + j * pt.gkv][n]);
-                }
-            }
-            const float wf = (m_run == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(m_run - M);
 #pragma unroll
             for (int c = 0; c < T::kOMfma; ++c) {
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
-                    sm_o[wave][n * D + T::kVBytes * (4 * g + r) + c] = oacc[c][r] * wf;
+                    sm_o[wave][n * D + T::kVBytes * (4 * g + r) + c] = oacc[c][r];
                 }
             }
         }
         __syncthreads();
+        // Loops over the waves of one kv head run over all kDecWaves slots
+        // with a predicate, unrolled, so their LDS reads issue together.
+        const int kl   = wave % pt.gkv;
         const int kvh0 = kvh - kl;   // first kv head of the workgroup's group
         for (int e = tid; e < pt.gkv * G * (D / 4); e += kDecThreads) {
             const int hg = e / (D / 4);   // (kv head of the group, q head) pair
             const int el = hg % pt.gkv;
             const int h  = hg / pt.gkv;
             const int d0 = 4 * (e - hg * (D / 4));
-            f32x4     a  = {0.f, 0.f, 0.f, 0.f};
+            float     M  = -INFINITY;
 #pragma unroll
             for (int j = 0; j < kDecWaves; ++j) {
                 if (j < wpk) {
-                    a += *reinterpret_cast<const f32x4*>(&sm_o[el + j * pt.gkv][h * D + d0]);
+                    M = fmaxf(M, sm_m[el + j * pt.gkv][h]);
+                }
+            }
+            f32x4 a = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int j = 0; j < kDecWaves; ++j) {
+                if (j < wpk) {
+                    const float mw = sm_m[el + j * pt.gkv][h];
+                    const float w  = (mw == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(mw - M);
+                    a += *reinterpret_cast<const f32x4*>(&sm_o[el + j * pt.gkv][h * D + d0]) * w;
                 }
             }
             const int64_t slot = static_cast<int64_t>((kvh0 + el) * G + h) * num_splits + si;
