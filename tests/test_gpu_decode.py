@@ -158,6 +158,10 @@ def test_long_splits_ragged_tail():
     (12345, 16, 4, 128, 128), (3000, 32, 8, 128, 128), (33, 32, 8, 64, 128),
     (20000, 32, 8, 64, 64), (9001, 16, 4, 128, 64), (20000, 32, 8, 64, 256),
     (9001, 16, 4, 128, 256),
+    # split counts whose grid is laid out for the fewest rounds (96 -> 4 kv
+    # heads per workgroup, 160 / 192 / 224 -> 8)
+    (9000, 24, 8, 96, 128), (5000, 24, 8, 192, 128), (20000, 32, 8, 160, 128),
+    (7001, 24, 8, 224, 64),
 ])
 def test_grouped_workgroups(ctx, hq, hkv, splits, d):
     """Launches with fewer (kv head, split) units than one round of wave
