@@ -159,7 +159,8 @@ def test_long_splits_ragged_tail():
     (20000, 32, 8, 64, 64), (9001, 16, 4, 128, 64), (20000, 32, 8, 64, 256),
     (9001, 16, 4, 128, 256),
     # split counts whose grid is laid out for the fewest rounds (96 -> 4 kv
-    # heads per workgroup, 160 / 192 / 224 -> 8)
+    # heads per workgroup; 160 / 192 / 224 -> one wave per kv head, i.e. the
+    # solo layout)
     (9000, 24, 8, 96, 128), (5000, 24, 8, 192, 128), (20000, 32, 8, 160, 128),
     (7001, 24, 8, 224, 64),
 ])
