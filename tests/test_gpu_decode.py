@@ -354,6 +354,38 @@ def test_decode_append_fused(cache_len, hq, hkv, d, splits):
     assert mx <= MAX_ABS and mean <= 1e-3, (mx, mean)
 
 
+@pytest.mark.parametrize("splits", [1, 3, 32, 96, 160, 256, 300])
+@pytest.mark.parametrize("cache_len", [0, 33, 1000, 5000])
+def test_decode_append_partition_sweep(splits, cache_len):
+    """Fused append + decode over the launch layouts a split count selects
+    (cooperative groups of 1/2/4 kv heads, the solo layout, the appended
+    key's own split, XCD-local placement) at depths on either side of one
+    tile per split: the cache row is the append kernel's and the output
+    matches the oracle."""
+    hq, hkv, d = 24, 8, 128
+    scale = np.float32(1.0 / np.sqrt(d))
+    total = cache_len + 1
+    _, _, k8, v8, ks, vs = make_cache(total, hkv, d, kind="normal", seed=splits + cache_len)
+    kn = O.normal_bf16((hkv, d), 6000 + splits)
+    vn = O.normal_bf16((hkv, d), 7000 + splits)
+    q = O.normal_bf16((hq, d), 8000 + cache_len)
+    kc, vc, ksd, vsd = u8_dev(k8), u8_dev(v8), f32_dev(ks), f32_dev(vs)
+    out = torch.empty((hq, d), dtype=torch.bfloat16, device=DEV)
+    partial = R.new_flash_split_scratch(hq, d, splits)
+    step(f"decode+append sweep ctx={total} splits={splits}")
+    R.flash_decode_append_split_bf16(out, bf16_dev(q), kc, vc, ksd, vsd, bf16_dev(kn),
+                                     bf16_dev(vn), partial, splits, int_dev(cache_len), hq, hkv,
+                                     d, scale)
+    sync()
+    rows = slice(cache_len * hkv, total * hkv)
+    wk, wks = O.quantize_kv_fp8(kn, d)
+    gk, gv = kc.cpu().numpy(), vc.cpu().numpy()
+    gks, gvs = ksd.cpu().numpy(), vsd.cpu().numpy()
+    assert np.array_equal(gk[rows], wk)
+    assert np.array_equal(gks[rows].view(np.uint32), wks.view(np.uint32))
+    check(bf16_host(out), q, gk, gv, gks, gvs, cache_len, hq, hkv, d, scale)
+
+
 @pytest.mark.parametrize("d", [64, 128, 256])
 def test_decode_append_fused_special_values(d):
     """The fused entry's quantizer on rows the append kernel's own tests cover
