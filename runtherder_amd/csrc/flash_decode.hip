@@ -31,7 +31,9 @@
 //      - fewer units (e.g. 64 splits x 8 kv heads): one workgroup per
 //        (group of kv heads, split), sized so the grid fills the chip; the
 //        waves of one kv head take every (8 / kvg)-th tile of the split
-//        and merge in LDS. Workgroups of one split land on one XCD.
+//        and merge in LDS (at most two tiles per split: the first wave of
+//        each kv head streams the split alone and the others leave).
+//        Workgroups of one split land on one XCD.
 //  * A second small kernel merges the splits of every (q head, 16-wide d
 //    slice): the head maximum from the m row, then weighted sums over a
 //    strided subset of splits per thread, lane exchanges, one LDS step. The scratch layout is the reference's ([Hq,S] m, [Hq,S]
@@ -781,6 +783,14 @@ __device__ __forceinline__ void decode_body(
     if (si >= n_live) {   // uniform per workgroup in coop mode
         return;
     }
+    // Coop workgroups whose splits hold at most two tiles (short contexts,
+    // uniform over the grid): the first wave of each kv head streams its
+    // split alone and stores its partial as a solo wave does; the others
+    // leave (no LDS merge, no barrier).
+    const bool lone = pt.coop && pt.base + (pt.rem > 0 ? 1 : 0) <= 2;
+    if (lone && wave >= pt.gkv) {
+        return;
+    }
     // Wave-uniform by construction; kept in scalar registers so that tile
     // addresses are a scalar base plus fixed per-lane offsets.
     const int kvc = __builtin_amdgcn_readfirstlane(nqb == 1 ? kvh : kvh / nqb);   // cache kv head
@@ -820,7 +830,7 @@ __device__ __forceinline__ void decode_body(
     // written); one wave of the owner split adds it from registers.
     const int  p_new   = n_keys - 1;
     const bool owner   = kAppend && (si == owner_si);
-    const bool virt    = owner && (!pt.coop || wave >= kDecWaves - pt.gkv);
+    const bool virt    = owner && (!pt.coop || lone || wave >= kDecWaves - pt.gkv);
     const int  k1      = owner ? p_new : min(split_tile(pt, si + 1) * kTileKeys, key_end);
     const int  n_tiles = (k1 - k0 + kTileKeys - 1) / kTileKeys;
     // The wave's cnt tiles of the split, tile_at(0 .. cnt - 1): all of them
@@ -828,9 +838,9 @@ __device__ __forceinline__ void decode_body(
     // tiles j, j + wpk, j + 2 wpk, ..., so the waves of a kv head read
     // neighbouring tiles at the same time.
     const int  wj        = pt.coop ? wave / pt.gkv : 0;
-    const int  wn        = pt.coop ? wpk : 1;
-    const int  cnt       = pt.coop ? (n_tiles - wj + wn - 1) / wn : n_tiles;
-    auto       tile_at   = [&](int i) { return pt.coop ? wj + i * wn : i; };
+    const int  wn        = (pt.coop && !lone) ? wpk : 1;
+    const int  cnt       = (pt.coop && !lone) ? (n_tiles - wj + wn - 1) / wn : n_tiles;
+    auto       tile_at   = [&](int i) { return (pt.coop && !lone) ? wj + i * wn : i; };
 
     // Q^T as the B operand: column n = q head n of the group. Columns past
     // G repeat head 0: their scores only ever mirror head 0's (so they never
@@ -1148,7 +1158,7 @@ __device__ __forceinline__ void decode_body(
     float*        part_m = partial;
     float*        part_l = partial + hs;
     float*        part_o = partial + 2 * hs;
-    if (pt.coop) {
+    if (pt.coop && !lone) {
         // Merge the waves of each kv head (waves kl, kl + gkv, ...): each
         // puts its m, l and unscaled O^T rows in LDS; after one barrier the
         // threads sum the rows along d with the weights 2^(m_w - M), which

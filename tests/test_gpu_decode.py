@@ -75,6 +75,25 @@ def test_split_count_sweep(splits):
     check(got, q, k8, v8, ks, vs, cache_len, hq, hkv, d, scale)
 
 
+@pytest.mark.parametrize("hq,hkv,d,splits", [
+    (24, 8, 128, 32), (24, 8, 128, 64), (24, 8, 128, 96), (32, 4, 64, 64), (16, 2, 256, 128),
+])
+@pytest.mark.parametrize("where", ["short", "edge", "past"])
+def test_grouped_workgroups_at_two_tiles_per_split(hq, hkv, d, splits, where):
+    """Grouped (cooperative) launches of 1, 2 and 4 kv heads per workgroup
+    on both sides of two 32-key tiles per split: up to two, the first wave
+    of each kv head streams its split alone; one key more and the waves of
+    a kv head share the tiles and merge in LDS."""
+    n_keys = {"short": 33, "edge": 64 * splits, "past": 64 * splits + 1}[where]
+    cache_len = n_keys - 1
+    scale = np.float32(1.0 / np.sqrt(d))
+    q = O.normal_bf16((hq, d), 17 + splits)
+    _, _, k8, v8, ks, vs = make_cache(n_keys, hkv, d, kind="normal", seed=n_keys)
+    step(f"grouped decode ctx={n_keys} splits={splits} hq={hq} hkv={hkv} d={d}")
+    got = gpu_decode(q, k8, v8, ks, vs, cache_len, hq, hkv, d, splits, scale)
+    check(got, q, k8, v8, ks, vs, cache_len, hq, hkv, d, scale)
+
+
 @pytest.mark.parametrize("splits", [1, 16, 64])
 def test_q_heads_of_extreme_magnitude(splits):
     """q heads scaled from zero and bf16 subnormals up to 2^6: scores several
