@@ -405,6 +405,39 @@ def test_decode_append_partition_sweep(splits, cache_len):
     check(bf16_host(out), q, gk, gv, gks, gvs, cache_len, hq, hkv, d, scale)
 
 
+@pytest.mark.parametrize("splits", [32, 64, 96])
+@pytest.mark.parametrize("extra", [0, 1, 64])
+def test_decode_append_grouped_own_split_edge(splits, extra):
+    """Grouped launches (1, 2 and 4 kv heads per workgroup) of the fused
+    append + decode at the edge of the appended key's own split: up to
+    64 * (splits - 1) cache keys the key takes a split of its own and every
+    other split one or two tiles; one key more and it joins the last split;
+    a tile more and the waves of a kv head share the tiles again."""
+    cache_len = 64 * (splits - 1) + extra
+    hq, hkv, d = 24, 8, 128
+    scale = np.float32(1.0 / np.sqrt(d))
+    total = cache_len + 1
+    _, _, k8, v8, ks, vs = make_cache(total, hkv, d, kind="normal", seed=splits + extra)
+    kn = O.normal_bf16((hkv, d), 6100 + splits)
+    vn = O.normal_bf16((hkv, d), 7100 + splits)
+    q = O.normal_bf16((hq, d), 8100 + extra)
+    kc, vc, ksd, vsd = u8_dev(k8), u8_dev(v8), f32_dev(ks), f32_dev(vs)
+    out = torch.empty((hq, d), dtype=torch.bfloat16, device=DEV)
+    partial = R.new_flash_split_scratch(hq, d, splits)
+    step(f"decode+append grouped own-split edge ctx={total} splits={splits}")
+    R.flash_decode_append_split_bf16(out, bf16_dev(q), kc, vc, ksd, vsd, bf16_dev(kn),
+                                     bf16_dev(vn), partial, splits, int_dev(cache_len), hq, hkv,
+                                     d, scale)
+    sync()
+    rows = slice(cache_len * hkv, total * hkv)
+    wk, wks = O.quantize_kv_fp8(kn, d)
+    gk, gv = kc.cpu().numpy(), vc.cpu().numpy()
+    gks, gvs = ksd.cpu().numpy(), vsd.cpu().numpy()
+    assert np.array_equal(gk[rows], wk)
+    assert np.array_equal(gks[rows].view(np.uint32), wks.view(np.uint32))
+    check(bf16_host(out), q, gk, gv, gks, gvs, cache_len, hq, hkv, d, scale)
+
+
 @pytest.mark.parametrize("d", [64, 128, 256])
 def test_decode_append_fused_special_values(d):
     """The fused entry's quantizer on rows the append kernel's own tests cover
