@@ -405,16 +405,16 @@ def test_decode_append_partition_sweep(splits, cache_len):
     check(bf16_host(out), q, gk, gv, gks, gvs, cache_len, hq, hkv, d, scale)
 
 
-@pytest.mark.parametrize("splits", [32, 64, 96])
+@pytest.mark.parametrize("splits,d", [(32, 128), (64, 128), (96, 128), (32, 64), (64, 256)])
 @pytest.mark.parametrize("extra", [0, 1, 64])
-def test_decode_append_grouped_own_split_edge(splits, extra):
+def test_decode_append_grouped_own_split_edge(splits, d, extra):
     """Grouped launches (1, 2 and 4 kv heads per workgroup) of the fused
     append + decode at the edge of the appended key's own split: up to
     64 * (splits - 1) cache keys the key takes a split of its own and every
     other split one or two tiles; one key more and it joins the last split;
     a tile more and the waves of a kv head share the tiles again."""
     cache_len = 64 * (splits - 1) + extra
-    hq, hkv, d = 24, 8, 128
+    hq, hkv = 24, 8
     scale = np.float32(1.0 / np.sqrt(d))
     total = cache_len + 1
     _, _, k8, v8, ks, vs = make_cache(total, hkv, d, kind="normal", seed=splits + extra)
@@ -424,7 +424,7 @@ def test_decode_append_grouped_own_split_edge(splits, extra):
     kc, vc, ksd, vsd = u8_dev(k8), u8_dev(v8), f32_dev(ks), f32_dev(vs)
     out = torch.empty((hq, d), dtype=torch.bfloat16, device=DEV)
     partial = R.new_flash_split_scratch(hq, d, splits)
-    step(f"decode+append grouped own-split edge ctx={total} splits={splits}")
+    step(f"decode+append grouped own-split edge ctx={total} splits={splits} d={d}")
     R.flash_decode_append_split_bf16(out, bf16_dev(q), kc, vc, ksd, vsd, bf16_dev(kn),
                                      bf16_dev(vn), partial, splits, int_dev(cache_len), hq, hkv,
                                      d, scale)
