@@ -24,8 +24,8 @@
 //  * Partitions (see DecPartition):
 //      - num_splits * Hkv >= 8 * CUs units: one WAVE per (kv head, split)
 //        unit. A workgroup holds the kv heads of one split (its waves share
-//        the interleaved scale lines in L1), or, when every split holds one
-//        tile, 8 splits of one kv head S/8 apart on one XCD (so the merge
+//        the interleaved scale lines in L1), or, when no split holds more
+//        than two tiles, 8 splits of one kv head S/8 apart on one XCD (so the merge
 //        reads that XCD's L2); waves never wait for each other and each
 //        writes its own partial.
 //      - fewer units (e.g. 64 splits x 8 kv heads): one workgroup per
