@@ -2,7 +2,11 @@
 // n_new == 1 runs the split-K flash decode with backend-owned scratch, n_new > 1
 // the MFMA flash prefill. The split count is chosen for the device at
 // construction (enough (kv head, split) workgroups to fill every CU) instead of
-// the reference's fixed 32.
+// the reference's fixed 32. Calls of 2 .. kPrefillSplitTokens tokens on shapes
+// the MFMA decode kernel serves run rth_attn_prefill_split over the same
+// scratch with num_splits / (2 n_new) splits (no reference counterpart: a few
+// tokens after a long cache as split-K decode; 16 tokens after 8K keys 209 ->
+// 36 us per call, at an empty cache up to ~3 us slower).
 #pragma once
 
 #include <runtherder/attention/backend.h>
@@ -65,6 +69,8 @@ public:
                                         hipStream_t           stream);
 
     [[nodiscard]] int num_splits() const noexcept { return num_splits_; }
+
+    static constexpr int kPrefillSplitTokens = 16;
 
 private:
     AttnConfig                     config_;

@@ -1,6 +1,6 @@
 """MI355X-native attention hot path of the Runtherder engine.
 
-Hand-written gfx950 HIP kernels (causal flash prefill on bf16 MFMA, split-K
+Hand-written gfx950 HIP kernels (causal flash prefill on MFMA, split-K
 GQA flash decode, FP8 E4M3 KV append/quantize) behind a C ABI
 (include/rth_attn.h, libruntherder_attn.so), with the reference engine's
 C++20 interface in include/runtherder/ and a torch-tensor front end in
@@ -30,6 +30,8 @@ from .ops import (  # noqa: F401
     flash_decode_split_bf16,
     flash_decode_split_bf16_noalloc,
     flash_prefill_bf16,
+    flash_prefill_split_bf16,
+    PREFILL_SPLIT_MAX_TOKENS,
     flash_split_scratch_floats,
     make_attention_backend,
     new_flash_split_scratch,

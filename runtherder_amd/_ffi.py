@@ -66,6 +66,11 @@ _SIGNATURES = {
                                                          ctypes.c_float, _vp]),
     "rth_attn_prefill_paged": (_c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_int, _c_int, _vp,
                                         _c_int, _c_int, _c_int, ctypes.c_float, _vp]),
+    "rth_attn_prefill_split": (_c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_int, _c_int, _vp,
+                                        _c_int, _c_int, _c_int, ctypes.c_float, _vp]),
+    "rth_attn_prefill_split_paged": (_c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_int, _vp,
+                                              _c_int, _c_int, _vp, _c_int, _c_int, _c_int,
+                                              ctypes.c_float, _vp]),
 }
 
 _lib: ctypes.CDLL | None = None

@@ -135,6 +135,29 @@ bool use_mfma_decode(int num_q_heads, int num_kv_heads, int head_dim) {
     const int shift = block_shift_of(bs);                                          \
     RTH_REQUIRE(shift >= 0, "block_size must be a power of two >= 32")
 
+int prefill_split_common(uint16_t* out, const uint16_t* q, const uint8_t* k, const uint8_t* v,
+                         const float* k_scale, const float* v_scale, const int* block_table,
+                         int shift, float* partial, int num_splits, int n_new,
+                         const int* cache_len, int num_q_heads, int num_kv_heads,
+                         int head_dim, float scale, void* stream, const char* what) {
+    if (int rc = check_attn(out, q, k, v, k_scale, v_scale, cache_len)) {
+        return rc;
+    }
+    RTH_REQUIRE(partial != nullptr, "partial must not be null");
+    RTH_REQUIRE(n_new >= 1 && n_new <= rth::kPrefillSplitMaxTokens, "n_new must be in [1, 64]");
+    RTH_REQUIRE(num_splits >= 1 && num_splits <= 65536, "num_splits must be in [1, 65536]");
+    if (int rc = check_heads(num_q_heads, num_kv_heads)) {
+        return rc;
+    }
+    RTH_REQUIRE(rth::decode_mfma_supported(num_q_heads, num_kv_heads, head_dim),
+                "rth_attn_prefill_split: head_dim 64/128/256 with q-head groups the MFMA "
+                "decode kernel serves (rth_decode_path == RTH_DECODE_MFMA)");
+    return check_hip(rth::flash_prefill_split_launch(out, q, k, v, k_scale, v_scale, partial,
+                                                     num_splits, n_new, cache_len, num_q_heads,
+                                                     num_kv_heads, head_dim, scale,
+                                                     as_stream(stream), block_table, shift),
+                     what);
+}
 }  // namespace
 
 extern "C" {
@@ -548,6 +571,28 @@ int rth_attn_prefill(uint16_t* out, const uint16_t* q, const uint8_t* k,
                                                cache_len, num_q_heads, num_kv_heads,
                                                head_dim, scale, as_stream(stream)),
                      "rth_attn_prefill");
+}
+
+int rth_attn_prefill_split(uint16_t* out, const uint16_t* q, const uint8_t* k,
+                           const uint8_t* v, const float* k_scale, const float* v_scale,
+                           float* partial, int num_splits, int n_new, const int* cache_len,
+                           int num_q_heads, int num_kv_heads, int head_dim, float scale,
+                           void* stream) {
+    return prefill_split_common(out, q, k, v, k_scale, v_scale, nullptr, 0, partial,
+                                num_splits, n_new, cache_len, num_q_heads, num_kv_heads,
+                                head_dim, scale, stream, "rth_attn_prefill_split");
+}
+
+int rth_attn_prefill_split_paged(uint16_t* out, const uint16_t* q, const uint8_t* k,
+                                 const uint8_t* v, const float* k_scale,
+                                 const float* v_scale, const int* block_table,
+                                 int block_size, float* partial, int num_splits, int n_new,
+                                 const int* cache_len, int num_q_heads, int num_kv_heads,
+                                 int head_dim, float scale, void* stream) {
+    RTH_PAGED_ARGS(block_table, block_size, shift);
+    return prefill_split_common(out, q, k, v, k_scale, v_scale, block_table, shift, partial,
+                                num_splits, n_new, cache_len, num_q_heads, num_kv_heads,
+                                head_dim, scale, stream, "rth_attn_prefill_split_paged");
 }
 
 int rth_attn_naive(uint16_t* out, const uint16_t* q, const uint8_t* k,

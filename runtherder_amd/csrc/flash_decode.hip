@@ -630,7 +630,13 @@ __device__ __forceinline__ void quantize_new_token(TileRaw<D>& vt, const uint16_
 // kNorm (with kRope): before the rotation, q rows and the appended k row
 // are RMS-normalized per head with the q_norm / k_norm gains (Qwen3's order,
 // rmsnorm_vec's arithmetic and reduction order).
-template <int D, bool kAppend, bool kPaged, bool kRope, bool kNorm = false>
+// kMulti (not with kAppend): n_tok query tokens of one causal prefill call
+// whose keys are all in the cache (cache_len keys before them): `hkv`
+// counts virtual heads (token, cache head, q block) in that order of
+// significance, `hq` the q heads of all tokens (q and out are [n_tok, Hq, D],
+// so virtual q head t * Hq + h is row t, head h), and token t attends to the
+// first *cache_len + t + 1 keys.
+template <int D, bool kAppend, bool kPaged, bool kRope, bool kNorm = false, bool kMulti = false>
 __device__ __forceinline__ void decode_body(
     const uint16_t* __restrict__ q, const uint8_t* __restrict__ k,
     const uint8_t* __restrict__ v, const float* __restrict__ ks,
@@ -641,9 +647,10 @@ __device__ __forceinline__ void decode_body(
     const int* __restrict__ block_table, int block_shift, int kvg, int nqb,
     const int* __restrict__ positions, const float* __restrict__ inv_freq,
     const uint16_t* __restrict__ q_norm = nullptr, const uint16_t* __restrict__ k_norm = nullptr,
-    float eps = 0.0f) {
+    float eps = 0.0f, int n_tok = 1) {
     using T = DecTraits<D>;
     static_assert(!kRope || kAppend, "the RoPE variant is the fused decode step");
+    static_assert(!kMulti || !kAppend, "the multi-token kernel attends to cached keys only");
     static_assert(!kNorm || kRope, "the q/k norm runs before the RoPE");
 
     __shared__ __attribute__((aligned(16))) float sm_sc[kDecWaves][64];
@@ -664,7 +671,7 @@ __device__ __forceinline__ void decode_body(
     const int g    = lane >> 4;
     const int bid  = static_cast<int>(blockIdx.x);
 
-    const int          n_keys = *cache_len + 1;
+    const int          n_keys = *cache_len + (kMulti ? n_tok : 1);
     DecPartition pt = dec_partition(n_keys, num_splits, kvg);
     // Append calls with at most two cache tiles per split
     // when one split is kept back: the appended key gets that split of its
@@ -799,8 +806,16 @@ __device__ __forceinline__ void decode_body(
     }
     // Wave-uniform by construction; kept in scalar registers so that tile
     // addresses are a scalar base plus fixed per-lane offsets.
-    const int kvc = __builtin_amdgcn_readfirstlane(nqb == 1 ? kvh : kvh / nqb);   // cache kv head
-    const int hkc = __builtin_amdgcn_readfirstlane(nqb == 1 ? hkv : hkv / nqb);   // cache kv heads
+    int kvc_v = nqb == 1 ? kvh : kvh / nqb;   // cache kv head (kMulti: token-major)
+    int hkc_v = nqb == 1 ? hkv : hkv / nqb;   // cache kv heads (kMulti: x n_tok)
+    if constexpr (kMulti) {
+        hkc_v /= n_tok;
+        const int tok = kvc_v / hkc_v;
+        kvc_v -= tok * hkc_v;
+        key_end = n_keys - (n_tok - 1 - tok);   // this token's causal limit
+    }
+    const int kvc = __builtin_amdgcn_readfirstlane(kvc_v);
+    const int hkc = __builtin_amdgcn_readfirstlane(hkc_v);
     // The appended row's bf16 words, issued before the stream (D <= 128: the
     // 40 VGPRs they hold through the stream spill the D = 256 kernels). Plain
     // loads, not loads inside the owner branch: a branch-merged load makes the
@@ -1273,6 +1288,21 @@ __global__ __launch_bounds__(kDecThreads) void flash_decode_kernel(
                                            nullptr);
 }
 
+// A causal prefill call of a few tokens over a long cache as split-K decode:
+// every (token, kv head) a virtual kv head (see decode_body's kMulti).
+template <int D, bool kPaged>
+__global__ __launch_bounds__(kDecThreads) void flash_decode_multi_kernel(
+    const uint16_t* __restrict__ q, const uint8_t* __restrict__ k,
+    const uint8_t* __restrict__ v, const float* __restrict__ ks,
+    const float* __restrict__ vs, float* __restrict__ partial, int num_splits,
+    const int* __restrict__ cache_len, int hq, int hkv, float scale_log2,
+    const int* __restrict__ block_table, int block_shift, int kvg, int nqb, int n_tok) {
+    decode_body<D, false, kPaged, false, false, true>(
+        q, k, v, ks, vs, partial, num_splits, cache_len, hq, hkv, scale_log2, nullptr, nullptr,
+        nullptr, nullptr, nullptr, nullptr, block_table, block_shift, kvg, nqb, nullptr, nullptr,
+        nullptr, nullptr, 0.0f, n_tok);
+}
+
 // The decode step with RoPE fused: rope of q and of the appended k row, the
 // append, and the split partials (the merge kernel follows as usual).
 template <int D, bool kPaged>
@@ -1356,7 +1386,7 @@ __device__ __forceinline__ float quad_group_sum(float v) {
 template <int D>
 __global__ __launch_bounds__(kCombineThreads) void flash_decode_combine_kernel(
     uint16_t* __restrict__ out, const float* __restrict__ partial, int num_splits,
-    const int* __restrict__ cache_len, int hq, int kvg, int xl_g, int append) {
+    const int* __restrict__ cache_len, int hq, int kvg, int xl_g, int append, int n_tok) {
     constexpr int kQuads  = kCombineSlice / 4;
     constexpr int kGroups = kCombineThreads / kQuads;
     constexpr int kCWaves = kCombineThreads / kWave;
@@ -1412,7 +1442,7 @@ __global__ __launch_bounds__(kCombineThreads) void flash_decode_combine_kernel(
     for (int e = 0; e < 4; ++e) {
         mr[e] = part_m[min(lane + kWave * e, num_splits - 1)];
     }
-    const int n_keys = *cache_len + 1;
+    const int n_keys = *cache_len + n_tok;   // the last (or only) token's keys
     // Live slots: as the split kernel derives them (an append call's key may
     // hold a slot of its own).
     const int cache_t = (n_keys + kTileKeys - 2) / kTileKeys;
@@ -1752,7 +1782,7 @@ hipError_t launch_decode_valu(uint16_t* out, const uint16_t* q, const uint8_t* k
     hipLaunchKernelGGL(flash_decode_combine_kernel<D>,
                        dim3(static_cast<unsigned>(hq), static_cast<unsigned>(D / kCombineSlice)),
                        dim3(kCombineThreads), 0, stream, out, partial, num_splits, cache_len,
-                       hq, 0, 0, 0);
+                       hq, 0, 0, 0, 1);
     return hipGetLastError();
 }
 
@@ -1822,7 +1852,47 @@ hipError_t launch_decode(uint16_t* out, const uint16_t* q, const uint8_t* k,
                        dim3(kCombineThreads), 0, stream, out, partial, num_splits,
                        cache_len, hq, kvg,
                        (kvg == 0 && dec_xcd_local(hkv_v, num_splits)) ? hq / hkv_v : 0,
-                       k_new != nullptr ? 1 : 0);
+                       k_new != nullptr ? 1 : 0, 1);
+    return hipGetLastError();
+}
+
+// A causal prefill call of n_tok tokens over the cache as split-K decode:
+// the split kernel over n_tok x Hkv (x q blocks) virtual kv heads, then the
+// merge over the n_tok x Hq rows of out. Scratch: the decode layout for
+// n_tok * Hq q heads.
+template <int D, bool kPaged>
+hipError_t launch_prefill_split(uint16_t* out, const uint16_t* q, const uint8_t* k,
+                                const uint8_t* v, const float* ks, const float* vs,
+                                float* partial, int num_splits, int n_tok,
+                                const int* cache_len, int hq, int hkv, float scale,
+                                const int* block_table, int block_shift, hipStream_t stream) {
+    int        cus = 0;
+    hipError_t ce  = device_cu_count(&cus);
+    if (ce != hipSuccess) {
+        return ce;
+    }
+    const int nqb = dec_q_blocks(hq, hkv, D);
+    if (nqb == 0) {
+        return hipErrorInvalidValue;
+    }
+    const int  hq_v  = hq * n_tok;
+    const int  hkv_v = hkv * nqb * n_tok;
+    const int  kvg   = dec_group_kv(num_splits, hkv_v, cus);
+    const int  n_wgs = dec_workgroups(num_splits, hkv_v, kvg);
+    hipLaunchKernelGGL((flash_decode_multi_kernel<D, kPaged>), dim3(static_cast<unsigned>(n_wgs)),
+                       dim3(kDecThreads), 0, stream, q, k, v, ks, vs, partial, num_splits,
+                       cache_len, hq_v, hkv_v, scale * kLog2e, block_table, block_shift, kvg,
+                       nqb, n_tok);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) {
+        return e;
+    }
+    hipLaunchKernelGGL(flash_decode_combine_kernel<D>,
+                       dim3(static_cast<unsigned>(hq_v), static_cast<unsigned>(D / kCombineSlice)),
+                       dim3(kCombineThreads), 0, stream, out, partial, num_splits, cache_len,
+                       hq_v, kvg,
+                       (kvg == 0 && dec_xcd_local(hkv_v, num_splits)) ? hq_v / hkv_v : 0, 0,
+                       n_tok);
     return hipGetLastError();
 }
 
@@ -1900,6 +1970,34 @@ hipError_t flash_decode_launch(uint16_t* out, const uint16_t* q,
         RTH_DEC_CASE(128)
         RTH_DEC_CASE(256)
 #undef RTH_DEC_CASE
+        default:
+            return hipErrorInvalidValue;
+    }
+}
+
+hipError_t flash_prefill_split_launch(uint16_t* out, const uint16_t* q, const uint8_t* k,
+                                     const uint8_t* v, const float* k_scale,
+                                     const float* v_scale, float* partial, int num_splits,
+                                     int n_new, const int* cache_len, int num_q_heads,
+                                     int num_kv_heads, int head_dim, float scale,
+                                     hipStream_t stream, const int* block_table,
+                                     int block_shift) {
+    const bool paged = block_table != nullptr;
+    switch (head_dim) {
+#define RTH_PFS_CASE(DD)                                                                      \
+    case DD:                                                                                  \
+        return paged ? launch_prefill_split<DD, true>(out, q, k, v, k_scale, v_scale, partial, \
+                                                      num_splits, n_new, cache_len,           \
+                                                      num_q_heads, num_kv_heads, scale,       \
+                                                      block_table, block_shift, stream)       \
+                     : launch_prefill_split<DD, false>(out, q, k, v, k_scale, v_scale,        \
+                                                       partial, num_splits, n_new, cache_len, \
+                                                       num_q_heads, num_kv_heads, scale,      \
+                                                       nullptr, 0, stream);
+        RTH_PFS_CASE(64)
+        RTH_PFS_CASE(128)
+        RTH_PFS_CASE(256)
+#undef RTH_PFS_CASE
         default:
             return hipErrorInvalidValue;
     }

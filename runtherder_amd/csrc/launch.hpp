@@ -60,6 +60,19 @@ hipError_t flash_decode_launch(uint16_t* out, const uint16_t* q,
                                const uint16_t* q_norm = nullptr,
                                const uint16_t* k_norm = nullptr, float eps = 0.0f);
 
+// A causal prefill call of n_new tokens after *cache_len cached keys (their
+// K/V already in the cache) as split-K decode over n_new x Hkv virtual kv
+// heads: the shapes decode_mfma_supported accepts; partial holds
+// decode_scratch_floats(n_new * Hq, D, num_splits) floats.
+constexpr int kPrefillSplitMaxTokens = 64;
+hipError_t flash_prefill_split_launch(uint16_t* out, const uint16_t* q, const uint8_t* k,
+                                     const uint8_t* v, const float* k_scale,
+                                     const float* v_scale, float* partial, int num_splits,
+                                     int n_new, const int* cache_len, int num_q_heads,
+                                     int num_kv_heads, int head_dim, float scale,
+                                     hipStream_t stream, const int* block_table = nullptr,
+                                     int block_shift = 0);
+
 // The VALU split kernel + merge: head_dim in {32, 64, 128, 256, 512}, any
 // GQA group (no paging, no fused append). The decode entry points use it for
 // the shapes decode_mfma_supported rejects.

@@ -41,6 +41,23 @@ void AdaptiveAttention::run(__hip_bfloat16* out, const __hip_bfloat16* q, const 
     auto* k  = reinterpret_cast<const std::uint8_t*>(kv.k);
     auto* v  = reinterpret_cast<const std::uint8_t*>(kv.v);
     const bool paged = kv.block_table != nullptr;
+    if (n_new >= 2 && n_new <= kPrefillSplitTokens &&
+        rth_decode_path(config_.num_q_heads, config_.num_kv_heads, config_.head_dim) ==
+            RTH_DECODE_MFMA) {
+        const int splits = num_splits_ / (2 * n_new) > 1 ? num_splits_ / (2 * n_new) : 1;
+        if (paged) {
+            RUNTHERDER_RTH_CHECK(rth_attn_prefill_split_paged(
+                o, qq, k, v, kv.k_scale, kv.v_scale, kv.block_table, kv.block_size,
+                partial_.get(), splits, n_new, cache_len, config_.num_q_heads,
+                config_.num_kv_heads, config_.head_dim, config_.scale, stream));
+        } else {
+            RUNTHERDER_RTH_CHECK(rth_attn_prefill_split(
+                o, qq, k, v, kv.k_scale, kv.v_scale, partial_.get(), splits, n_new, cache_len,
+                config_.num_q_heads, config_.num_kv_heads, config_.head_dim, config_.scale,
+                stream));
+        }
+        return;
+    }
     if (n_new == 1) {
         if (paged) {
             RUNTHERDER_RTH_CHECK(rth_attn_decode_split_paged(

@@ -187,6 +187,26 @@ def flash_prefill_bf16(out, q, k, v, k_scale, v_scale, n_new, cache_len, num_q_h
               _stream(stream))
 
 
+PREFILL_SPLIT_MAX_TOKENS = 64
+
+
+def flash_prefill_split_bf16(out, q, k, v, k_scale, v_scale, partial, num_splits, n_new,
+                             cache_len, num_q_heads, num_kv_heads, head_dim, scale,
+                             stream=None):
+    """flash_prefill_bf16 for a few tokens after a long cache, as split-K
+    decode over (token, kv head) units (no reference counterpart; the
+    reference walks every key serially per q tile, flash_prefill.cu:34-241).
+    partial: flash_split_scratch_floats(n_new * num_q_heads, head_dim,
+    num_splits) floats; 1 <= n_new <= PREFILL_SPLIT_MAX_TOKENS."""
+    _need(out, torch.bfloat16, "out"); _need(q, torch.bfloat16, "q")
+    _need(k, torch.uint8, "k"); _need(v, torch.uint8, "v")
+    _need(k_scale, torch.float32, "k_scale"); _need(v_scale, torch.float32, "v_scale")
+    _need(partial, torch.float32, "partial"); _need(cache_len, torch.int32, "cache_len")
+    _ffi.call("rth_attn_prefill_split", _p(out), _p(q), _p(k), _p(v), _p(k_scale),
+              _p(v_scale), _p(partial), num_splits, n_new, _p(cache_len), num_q_heads,
+              num_kv_heads, head_dim, float(scale), _stream(stream))
+
+
 def attention_causal_bf16(out, q, k, v, k_scale, v_scale, n_new, cache_len, num_q_heads,
                           num_kv_heads, head_dim, scale, stream=None):
     """reference include/runtherder/kernels/attention.cuh:21-34"""
@@ -421,10 +441,17 @@ class AttentionBackend:
         raise NotImplementedError
 
 
+PREFILL_SPLIT_TOKENS = 16
+
+
 class AdaptiveAttention(AttentionBackend):
     """reference src/attention/adaptive.cu: n_new == 1 -> split decode with
     backend-owned scratch, else flash prefill. Split count defaults to the
-    device's (kv head, split) fill count."""
+    device's (kv head, split) fill count. Calls of 2..PREFILL_SPLIT_TOKENS
+    tokens on shapes the MFMA decode kernel serves take the split-K prefill
+    (flash_prefill_split_bf16) over the same scratch, with num_splits //
+    (2 n_new) splits (no reference counterpart: per call, 16 tokens after
+    8K keys 209 -> 36 us; at an empty cache up to ~3 us slower)."""
 
     def __init__(self, config: AttnConfig, num_splits: int | None = None, device="cuda"):
         self.config = config
@@ -433,10 +460,24 @@ class AdaptiveAttention(AttentionBackend):
         self.partial = new_flash_split_scratch(config.num_q_heads, config.head_dim,
                                                self.num_splits, device=device)
 
+    def _split_prefill_splits(self, n_new):
+        c = self.config
+        if not 2 <= n_new <= PREFILL_SPLIT_TOKENS:
+            return 0
+        if decode_path(c.num_q_heads, c.num_kv_heads, c.head_dim) != DECODE_MFMA:
+            return 0
+        return max(1, self.num_splits // (2 * n_new))
+
     def run(self, out, q, kv, n_new, cache_len, stream=None):
         c = self.config
+        ps = self._split_prefill_splits(n_new)
         if kv.block_table is not None:
-            if n_new == 1:
+            if ps:
+                _ffi.call("rth_attn_prefill_split_paged", _p(out), _p(q), _p(kv.k), _p(kv.v),
+                          _p(kv.k_scale), _p(kv.v_scale), _p(kv.block_table), kv.block_size,
+                          _p(self.partial), ps, n_new, _p(cache_len), c.num_q_heads,
+                          c.num_kv_heads, c.head_dim, float(c.scale), _stream(stream))
+            elif n_new == 1:
                 _ffi.call("rth_attn_decode_split_paged", _p(out), _p(q), _p(kv.k), _p(kv.v),
                           _p(kv.k_scale), _p(kv.v_scale), _p(kv.block_table), kv.block_size,
                           _p(self.partial), self.num_splits, _p(cache_len), c.num_q_heads,
@@ -447,7 +488,11 @@ class AdaptiveAttention(AttentionBackend):
                           n_new, _p(cache_len), c.num_q_heads, c.num_kv_heads, c.head_dim,
                           float(c.scale), _stream(stream))
             return
-        if n_new == 1:
+        if ps:
+            flash_prefill_split_bf16(out, q, kv.k, kv.v, kv.k_scale, kv.v_scale, self.partial,
+                                     ps, n_new, cache_len, c.num_q_heads, c.num_kv_heads,
+                                     c.head_dim, c.scale, stream)
+        elif n_new == 1:
             flash_decode_split_bf16(out, q, kv.k, kv.v, kv.k_scale, kv.v_scale, self.partial,
                                     self.num_splits, cache_len, c.num_q_heads, c.num_kv_heads,
                                     c.head_dim, c.scale, stream)

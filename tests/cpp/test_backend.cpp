@@ -63,9 +63,11 @@ T* dev_alloc(size_t n) {
 
 int run_case(BackendKind kind, const char* name) {
     const int   L = 2, S = 256, Hq = 24, Hkv = 8, D = 128;
-    const int   prefill = 37, chunk = 29, steps = 5;
+    // chunk of 29: the flash prefill; chunk of 4: AdaptiveAttention's split-K
+    // prefill of a few tokens; then one-token decode steps.
+    const int   prefill = 37, chunk = 29, small = 4, steps = 5;
     const float scale = 1.0f / std::sqrt(static_cast<float>(D));
-    const int   total = prefill + chunk + steps;
+    const int   total = prefill + chunk + small + steps;
 
     KVCache cache(L, S, Hkv, D);
     auto    backend = make_attention_backend(kind, AttnConfig{Hq, Hkv, D, scale});
@@ -91,7 +93,7 @@ int run_case(BackendKind kind, const char* name) {
 
     int fails = 0;
     int start = 0;
-    std::vector<int> chunks = {prefill, chunk};
+    std::vector<int> chunks = {prefill, chunk, small};
     for (int i = 0; i < steps; ++i) {
         chunks.push_back(1);
     }
