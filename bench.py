@@ -364,6 +364,47 @@ def bench_rope_append(torch, R, stream, n=4096, iters=20):
     return res
 
 
+def bench_few_token_prefill(torch, R, stream, iters=10):
+    """A causal prefill call of a few tokens after a long cache (32Q/8KV,
+    head_dim 128): the flash prefill kernel (rth_attn_prefill, one workgroup
+    per q tile walking every key, as the reference's) against
+    AdaptiveAttention.run, which routes 2..16 tokens to the split-K prefill
+    over its scratch (rth_attn_prefill_split)."""
+    hq, hkv, d = 32, 8, 128
+    dev = torch.device("cuda:0")
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(7)
+    res = []
+    be = R.AdaptiveAttention(R.AttnConfig.for_heads(hq, hkv, d))
+    for clen in (8192, 32768):
+        total = clen + 16
+        cache = R.KVCache(1, total, hkv, d, device=dev)
+        p0 = torch.zeros(1, dtype=torch.int32, device=dev)
+        cl = torch.full((1,), clen, dtype=torch.int32, device=dev)
+        torch.cuda.synchronize()
+        with torch.cuda.stream(stream):
+            k = torch.randn((total, hkv, d), generator=gen, device=dev).to(torch.bfloat16)
+            v = torch.randn((total, hkv, d), generator=gen, device=dev).to(torch.bfloat16)
+            cache.append(0, k, v, total, p0)
+            view = cache.view(0)
+            for n in (4, 16):
+                q = torch.randn((n, hq, d), generator=gen, device=dev).to(torch.bfloat16)
+                out = torch.empty_like(q)
+
+                def flash():
+                    R.flash_prefill_bf16(out, q, view.k, view.v, view.k_scale, view.v_scale, n,
+                                         cl, hq, hkv, d, d ** -0.5)
+
+                def adaptive():
+                    be.run(out, q, view, n, cl)
+                fu = graph_us(torch, stream, flash, iters)
+                au = graph_us(torch, stream, adaptive, iters)
+                res.append({"clen": clen, "n_new": n, "flash_prefill_us": round(fu, 2),
+                            "adaptive_split_us": round(au, 2), "speedup": round(fu / au, 1)})
+        del cache
+    return res
+
+
 def decode_kernel_sweep(torch, R, stream, points, quiet=False):
     """Per-call decode time of the headline step's call (the fused one-token
     K/V append + split kernel, then the merge kernel) at several context
@@ -658,6 +699,7 @@ def main() -> int:
     dec = bench_decode(torch, R, args, stream)
     pf = bench_prefill(torch, R, stream, n=args.prefill_n)
     ra = bench_rope_append(torch, R, stream, n=args.prefill_n)
+    few = bench_few_token_prefill(torch, R, stream)
     extra = extra_rooflines(torch, R, stream)
     cpu = None if args.no_cpu else cpu_baseline(torch, dec)
     cpu_pf = None if args.no_cpu else cpu_prefill_baseline()
@@ -706,6 +748,11 @@ def main() -> int:
         "rope_append": dict(ra, workload="config4 shapes: RoPE(q,k) + K/V FP8 append (and the "
                                          "Qwen3 q/k RMSNorm before it), fused entries vs the "
                                          "unfused launch sequences"),
+        "prefill_few_tokens": {
+            "unit": "us per call", "points": few,
+            "workload": "32Q/8KV head_dim 128: n_new = 4 / 16 tokens after 8192 / 32768 "
+                        "cached keys; the flash prefill kernel vs AdaptiveAttention.run "
+                        "(split-K prefill over (token, kv head) units for 2..16 tokens)"},
         "decode_step_unfused": {
             "value": round(dec["unfused_value"], 1), "unit": "GB/s",
             "ms_per_step": round(dec["unfused_ms_per_step"], 4),
