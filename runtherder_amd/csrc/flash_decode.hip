@@ -43,6 +43,7 @@
 // merge folds the first n_eff = min(splits, tiles) slots. n_keys =
 // *cache_len + 1 is read on device, so one launch configuration serves every
 // decode step (graph capturable).
+#include <algorithm>
 #include <mutex>
 
 #include "device_common.hpp"
@@ -631,11 +632,15 @@ __device__ __forceinline__ void quantize_new_token(TileRaw<D>& vt, const uint16_
 // are RMS-normalized per head with the q_norm / k_norm gains (Qwen3's order,
 // rmsnorm_vec's arithmetic and reduction order).
 // kMulti (not with kAppend): n_tok query tokens of one causal prefill call
-// whose keys are all in the cache (cache_len keys before them): `hkv`
-// counts virtual heads (token, cache head, q block) in that order of
-// significance, `hq` the q heads of all tokens (q and out are [n_tok, Hq, D],
-// so virtual q head t * Hq + h is row t, head h), and token t attends to the
-// first *cache_len + t + 1 keys.
+// whose keys are all in the cache (*cache_len keys before them). A virtual
+// kv head is (block of tb tokens, cache head, q block), in that order of
+// significance (`hkv` counts them); its G = hq / hkv MFMA columns are the
+// block's tokens x gb = G / tb q heads (column n: token n / gb, head n % gb),
+// so one pass over a key tile serves tb tokens. q and out are
+// [n_tok, hq_real, D]; the partials use the rows t * hq_real + h (the merge
+// runs over n_tok * hq_real rows). Token t attends to the first
+// *cache_len + t + 1 keys: a per-column limit in the tile mask; columns past
+// the block's tokens or G mirror column 0 and are never stored.
 template <int D, bool kAppend, bool kPaged, bool kRope, bool kNorm = false, bool kMulti = false>
 __device__ __forceinline__ void decode_body(
     const uint16_t* __restrict__ q, const uint8_t* __restrict__ k,
@@ -647,7 +652,7 @@ __device__ __forceinline__ void decode_body(
     const int* __restrict__ block_table, int block_shift, int kvg, int nqb,
     const int* __restrict__ positions, const float* __restrict__ inv_freq,
     const uint16_t* __restrict__ q_norm = nullptr, const uint16_t* __restrict__ k_norm = nullptr,
-    float eps = 0.0f, int n_tok = 1) {
+    float eps = 0.0f, int n_tok = 1, int hq_real = 0, int tb = 1) {
     using T = DecTraits<D>;
     static_assert(!kRope || kAppend, "the RoPE variant is the fused decode step");
     static_assert(!kMulti || !kAppend, "the multi-token kernel attends to cached keys only");
@@ -806,16 +811,38 @@ __device__ __forceinline__ void decode_body(
     }
     // Wave-uniform by construction; kept in scalar registers so that tile
     // addresses are a scalar base plus fixed per-lane offsets.
-    int kvc_v = nqb == 1 ? kvh : kvh / nqb;   // cache kv head (kMulti: token-major)
-    int hkc_v = nqb == 1 ? hkv : hkv / nqb;   // cache kv heads (kMulti: x n_tok)
+    int kvc_v = nqb == 1 ? kvh : kvh / nqb;   // cache kv head (kMulti: token-block major)
+    int hkc_v = nqb == 1 ? hkv : hkv / nqb;   // cache kv heads (kMulti: x token blocks)
+    [[maybe_unused]] int lim_lo = 0;          // kMulti: the block's first token's key limit
+    [[maybe_unused]] int gbm    = G;          // kMulti: q heads per token of a column block
     if constexpr (kMulti) {
-        hkc_v /= n_tok;
-        const int tok = kvc_v / hkc_v;
-        kvc_v -= tok * hkc_v;
-        key_end = n_keys - (n_tok - 1 - tok);   // this token's causal limit
+        hkc_v /= (n_tok + tb - 1) / tb;
+        const int tblk = kvc_v / hkc_v;
+        kvc_v -= tblk * hkc_v;
+        const int tok0 = tblk * tb;
+        key_end = n_keys - n_tok + min(tok0 + tb, n_tok);   // the block's last token's limit
+        lim_lo  = n_keys - n_tok + tok0 + 1;
+        gbm     = G / tb;
     }
     const int kvc = __builtin_amdgcn_readfirstlane(kvc_v);
     const int hkc = __builtin_amdgcn_readfirstlane(hkc_v);
+    // kMulti: output row of column col of virtual kv head vk (-1: padding).
+    [[maybe_unused]] auto mrow = [&](int vk, int col) -> int {
+        const int qbv = nqb == 1 ? 0 : vk % nqb;
+        const int vh  = nqb == 1 ? vk : vk / nqb;
+        const int tbk = vh / hkc;
+        const int t   = tbk * tb + col / gbm;
+        if (col >= G || t >= n_tok) {
+            return -1;
+        }
+        return t * hq_real + (vh - tbk * hkc) * (gbm * nqb) + qbv * gbm + col % gbm;
+    };
+    [[maybe_unused]] int row_n = 0;   // kMulti: this lane's column's row (-1: padding)
+    [[maybe_unused]] int lim_n = 0;   // kMulti: its key limit
+    if constexpr (kMulti) {
+        row_n = mrow(kvh, n);
+        lim_n = row_n < 0 ? lim_lo : lim_lo + (n / gbm);
+    }
     // The appended row's bf16 words, issued before the stream (D <= 128: the
     // 40 VGPRs they hold through the stream spill the D = 256 kernels). Plain
     // loads, not loads inside the owner branch: a branch-merged load makes the
@@ -870,7 +897,9 @@ __device__ __forceinline__ void decode_body(
     // its first K/V tile loads (measured 0.3-0.7 us per call at 8K).
     bf16x8 qop[T::kKSteps];
     {
-        const uint16_t* qr = q + static_cast<int64_t>(kvh * G + (n < G ? n : 0)) * D;
+        const int64_t   qrow = kMulti ? static_cast<int64_t>(row_n >= 0 ? row_n : mrow(kvh, 0))
+                                          : static_cast<int64_t>(kvh * G + (n < G ? n : 0));
+        const uint16_t* qr   = q + qrow * D;
 #pragma unroll
         for (int c = 0; c < T::kKChunks; ++c) {
 #pragma unroll
@@ -1007,7 +1036,17 @@ __device__ __forceinline__ void decode_body(
             x[r]     = s[0][r] * kf0[r];
             x[4 + r] = s[1][r] * kf1[r];
         }
-        if (kb + kTileKeys > klim) {  // ragged last tile of the split
+        if constexpr (kMulti) {
+            if (kb + kTileKeys > min(klim, lim_lo)) {  // a column's limit or the split's end
+                const int lim = min(klim, lim_n);
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    if (kb + key_of(g, j) >= lim) {
+                        x[j] = -INFINITY;
+                    }
+                }
+            }
+        } else if (kb + kTileKeys > klim) {  // ragged last tile of the split
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
                 if (kb + key_of(g, j) >= klim) {
@@ -1023,7 +1062,11 @@ __device__ __forceinline__ void decode_body(
             const float m_new = fmaxf(m_run, lmax);
             // A wave's first tile (nothing accumulated yet) needs no rescale.
             if (!__all(m_run == -INFINITY)) {
-                const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+                // kMulti: a column whose keys all lie past its limit keeps
+                // m = -inf (and l = 0) while others move.
+                const float alpha = (kMulti && m_new == -INFINITY)
+                                        ? 1.0f
+                                        : __builtin_amdgcn_exp2f(m_run - m_new);
                 l_run *= alpha;
 #pragma unroll
                 for (int c = 0; c < T::kOMfma; ++c) {
@@ -1033,9 +1076,10 @@ __device__ __forceinline__ void decode_body(
             m_run = m_new;
         }
         float p[8];
+        const float m_sub = (kMulti && m_run == -INFINITY) ? 0.0f : m_run;   // p = 0, not NaN
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
-            p[j] = __builtin_amdgcn_exp2f(x[j] - m_run);
+            p[j] = __builtin_amdgcn_exp2f(x[j] - m_sub);
         }
         l_run += ((p[0] + p[1]) + (p[2] + p[3])) + ((p[4] + p[5]) + (p[6] + p[7]));
 
@@ -1175,7 +1219,7 @@ __device__ __forceinline__ void decode_body(
     // with S = num_splits.
     l_run = wave_xor_sum(l_run, 16);
     l_run = wave_xor_sum(l_run, 32);
-    const int64_t hs     = static_cast<int64_t>(hq) * num_splits;
+    const int64_t hs     = static_cast<int64_t>(kMulti ? n_tok * hq_real : hq) * num_splits;
     float*        part_m = partial;
     float*        part_l = partial + hs;
     float*        part_o = partial + 2 * hs;
@@ -1224,8 +1268,11 @@ __device__ __forceinline__ void decode_body(
                     a += *reinterpret_cast<const f32x4*>(&sm_o[el + j * pt.gkv][h * D + d0]) * w;
                 }
             }
-            const int64_t slot = static_cast<int64_t>((kvh0 + el) * G + h) * num_splits + si;
-            *reinterpret_cast<f32x4*>(&part_o[slot * D + d0]) = a;
+            const int64_t row  = kMulti ? mrow(kvh0 + el, h) : (kvh0 + el) * G + h;
+            const int64_t slot = row * num_splits + si;
+            if (!kMulti || row >= 0) {
+                *reinterpret_cast<f32x4*>(&part_o[slot * D + d0]) = a;
+            }
         }
         if (tid < pt.gkv * G) {
             const int el = tid % pt.gkv;
@@ -1245,16 +1292,20 @@ __device__ __forceinline__ void decode_body(
                     L += (mw == -INFINITY) ? 0.0f : sm_l[el + j * pt.gkv][h] * __builtin_amdgcn_exp2f(mw - M);
                 }
             }
-            const int64_t slot = static_cast<int64_t>((kvh0 + el) * G + h) * num_splits + si;
-            part_m[slot]       = M;
-            part_l[slot]       = L;
+            const int64_t row  = kMulti ? mrow(kvh0 + el, h) : (kvh0 + el) * G + h;
+            const int64_t slot = row * num_splits + si;
+            if (!kMulti || row >= 0) {
+                part_m[slot] = M;
+                part_l[slot] = L;
+            }
         }
     } else {
         // Straight from the MFMA layout: lane (n, g) holds, for each r, the
         // kOMfma consecutive values d = kVBytes * (4g + r) + c of q head n
         // (oacc[c][r]), so it stores them as 16-byte runs with no LDS pass.
-        if (n < G) {
-            const int64_t slot = static_cast<int64_t>(kvh * G + n) * num_splits + si;
+        if (kMulti ? row_n >= 0 : n < G) {
+            const int64_t row  = kMulti ? row_n : kvh * G + n;
+            const int64_t slot = row * num_splits + si;
             float*        po   = part_o + slot * D;
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
@@ -1265,8 +1316,9 @@ __device__ __forceinline__ void decode_body(
                 }
             }
         }
-        if (g == 0 && n < G) {
-            const int64_t slot = static_cast<int64_t>(kvh * G + n) * num_splits + si;
+        if (g == 0 && (kMulti ? row_n >= 0 : n < G)) {
+            const int64_t row  = kMulti ? row_n : kvh * G + n;
+            const int64_t slot = row * num_splits + si;
             part_m[slot]       = m_run;
             part_l[slot]       = l_run;
         }
@@ -1296,11 +1348,12 @@ __global__ __launch_bounds__(kDecThreads) void flash_decode_multi_kernel(
     const uint8_t* __restrict__ v, const float* __restrict__ ks,
     const float* __restrict__ vs, float* __restrict__ partial, int num_splits,
     const int* __restrict__ cache_len, int hq, int hkv, float scale_log2,
-    const int* __restrict__ block_table, int block_shift, int kvg, int nqb, int n_tok) {
+    const int* __restrict__ block_table, int block_shift, int kvg, int nqb, int n_tok,
+    int hq_real, int tb) {
     decode_body<D, false, kPaged, false, false, true>(
         q, k, v, ks, vs, partial, num_splits, cache_len, hq, hkv, scale_log2, nullptr, nullptr,
         nullptr, nullptr, nullptr, nullptr, block_table, block_shift, kvg, nqb, nullptr, nullptr,
-        nullptr, nullptr, 0.0f, n_tok);
+        nullptr, nullptr, 0.0f, n_tok, hq_real, tb);
 }
 
 // The decode step with RoPE fused: rope of q and of the appended k row, the
@@ -1875,14 +1928,19 @@ hipError_t launch_prefill_split(uint16_t* out, const uint16_t* q, const uint8_t*
     if (nqb == 0) {
         return hipErrorInvalidValue;
     }
-    const int  hq_v  = hq * n_tok;
-    const int  hkv_v = hkv * nqb * n_tok;
+    // Tokens per virtual kv head: as many as fill the MFMA's 16 columns (and
+    // a wave's LDS staging row) with the block's q heads.
+    const int gb  = hq / hkv / nqb;
+    const int tb  = std::max(1, std::min({16 / gb, kMaxGroupD / (gb * D), n_tok}));
+    const int ntb = (n_tok + tb - 1) / tb;
+    const int  hq_v  = hq * n_tok;                 // rows of out and of the partials
+    const int  hkv_v = hkv * nqb * ntb;
     const int  kvg   = dec_group_kv(num_splits, hkv_v, cus);
     const int  n_wgs = dec_workgroups(num_splits, hkv_v, kvg);
     hipLaunchKernelGGL((flash_decode_multi_kernel<D, kPaged>), dim3(static_cast<unsigned>(n_wgs)),
                        dim3(kDecThreads), 0, stream, q, k, v, ks, vs, partial, num_splits,
-                       cache_len, hq_v, hkv_v, scale * kLog2e, block_table, block_shift, kvg,
-                       nqb, n_tok);
+                       cache_len, hkv_v * tb * gb, hkv_v, scale * kLog2e, block_table,
+                       block_shift, kvg, nqb, n_tok, hq, tb);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) {
         return e;
@@ -1891,8 +1949,9 @@ hipError_t launch_prefill_split(uint16_t* out, const uint16_t* q, const uint8_t*
                        dim3(static_cast<unsigned>(hq_v), static_cast<unsigned>(D / kCombineSlice)),
                        dim3(kCombineThreads), 0, stream, out, partial, num_splits, cache_len,
                        hq_v, kvg,
-                       (kvg == 0 && dec_xcd_local(hkv_v, num_splits)) ? hq_v / hkv_v : 0, 0,
-                       n_tok);
+                       (tb == 1 && kvg == 0 && dec_xcd_local(hkv_v, num_splits)) ? hq_v / hkv_v
+                                                                                 : 0,
+                       0, n_tok);
     return hipGetLastError();
 }
 

@@ -441,7 +441,7 @@ class AttentionBackend:
         raise NotImplementedError
 
 
-PREFILL_SPLIT_TOKENS = 16
+PREFILL_SPLIT_TOKENS = 32
 
 
 class AdaptiveAttention(AttentionBackend):
@@ -451,7 +451,8 @@ class AdaptiveAttention(AttentionBackend):
     tokens on shapes the MFMA decode kernel serves take the split-K prefill
     (flash_prefill_split_bf16) over the same scratch, with num_splits //
     (2 n_new) splits (no reference counterpart: per call, 16 tokens after
-    8K keys 209 -> 36 us; at an empty cache up to ~3 us slower)."""
+    8K keys 209 -> 21 us, 32 tokens 209 -> 30 us; at an empty cache up to
+    ~8 us slower)."""
 
     def __init__(self, config: AttnConfig, num_splits: int | None = None, device="cuda"):
         self.config = config
