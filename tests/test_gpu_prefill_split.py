@@ -38,7 +38,8 @@ def inputs(n_new, clen, hq, hkv, d, seed):
 
 
 # (n_new, clen, hq, hkv, d, splits): 2..64 tokens; caches from empty to 8K;
-# groups of 4 and 3 q heads, MQA (8), 32 (two q blocks), head_dim 64 / 256;
+# groups of 1, 2, 3, 4 and 6 q heads, MQA (8), 32 (two q blocks), head_dim
+# 64 / 256;
 # split counts that are and are not multiples of 8, more splits than tiles,
 # grouped (cooperative) and one-wave-per-unit launches.
 CASES = [
@@ -47,6 +48,11 @@ CASES = [
     (5, 333, 32, 8, 64, 32), (7, 600, 16, 2, 256, 16), (2, 50, 64, 2, 128, 32),
     (1, 500, 32, 8, 128, 256), (4, 4000, 8, 1, 128, 100), (16, 40, 32, 8, 128, 128),
     (13, 2047, 24, 8, 128, 19), (32, 4096, 32, 8, 128, 8),
+    # MHA (16 tokens per virtual head), groups of 2 (8) and 6 (2), head_dim
+    # 256 at 8 tokens per virtual head (its LDS staging row), a ragged last
+    # token block.
+    (37, 1500, 8, 8, 128, 16), (19, 700, 16, 8, 128, 32), (9, 900, 12, 2, 128, 64),
+    (20, 1234, 4, 4, 256, 16),
 ]
 
 
