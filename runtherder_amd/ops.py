@@ -441,7 +441,7 @@ class AttentionBackend:
         raise NotImplementedError
 
 
-PREFILL_SPLIT_TOKENS = 32
+PREFILL_SPLIT_TOKENS = 64
 
 
 class AdaptiveAttention(AttentionBackend):
@@ -450,9 +450,9 @@ class AdaptiveAttention(AttentionBackend):
     device's (kv head, split) fill count. Calls of 2..PREFILL_SPLIT_TOKENS
     tokens on shapes the MFMA decode kernel serves take the split-K prefill
     (flash_prefill_split_bf16) over the same scratch, with num_splits //
-    (2 n_new) splits (no reference counterpart: per call, 16 tokens after
-    8K keys 209 -> 21 us, 32 tokens 209 -> 30 us; at an empty cache up to
-    ~8 us slower)."""
+    (2 n_new) splits (no reference counterpart: per call, 16 / 64 tokens
+    after 8K keys 209 / 199 -> 18 / 35 us; at an empty cache up to ~2 us
+    slower)."""
 
     def __init__(self, config: AttnConfig, num_splits: int | None = None, device="cuda"):
         self.config = config

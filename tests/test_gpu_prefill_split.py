@@ -138,10 +138,10 @@ def test_prefill_split_rejects_bad_arguments():
                                    k, s, s, part, 4, 2, int_dev(0), hq, hkv, 32, 0.1)
 
 
-@pytest.mark.parametrize("n_new", [2, 32, 33])
+@pytest.mark.parametrize("n_new", [2, 64, 65])
 def test_adaptive_backend_routes_small_prefill(n_new):
-    """AdaptiveAttention.run: 2..32 tokens take the split-K prefill over the
-    backend's scratch, 33 the flash prefill; both match the oracle."""
+    """AdaptiveAttention.run: 2..64 tokens take the split-K prefill over the
+    backend's scratch, 65 the flash prefill; both match the oracle."""
     hq, hkv, d, clen = 32, 8, 128, 3000
     scale = np.float32(1.0 / np.sqrt(d))
     q, k8, v8, ks, vs = inputs(n_new, clen, hq, hkv, d, 500 + n_new)
