@@ -368,7 +368,7 @@ def bench_few_token_prefill(torch, R, stream, iters=10):
     """A causal prefill call of a few tokens after a long cache (32Q/8KV,
     head_dim 128): the flash prefill kernel (rth_attn_prefill, one workgroup
     per q tile walking every key, as the reference's) against
-    AdaptiveAttention.run, which routes 2..64 tokens to the split-K prefill
+    AdaptiveAttention.run, which routes 2..128 tokens to the split-K prefill
     over its scratch (rth_attn_prefill_split)."""
     hq, hkv, d = 32, 8, 128
     dev = torch.device("cuda:0")
@@ -377,7 +377,7 @@ def bench_few_token_prefill(torch, R, stream, iters=10):
     res = []
     be = R.AdaptiveAttention(R.AttnConfig.for_heads(hq, hkv, d))
     for clen in (8192, 32768):
-        total = clen + 64
+        total = clen + 128
         cache = R.KVCache(1, total, hkv, d, device=dev)
         p0 = torch.zeros(1, dtype=torch.int32, device=dev)
         cl = torch.full((1,), clen, dtype=torch.int32, device=dev)
@@ -387,7 +387,7 @@ def bench_few_token_prefill(torch, R, stream, iters=10):
             v = torch.randn((total, hkv, d), generator=gen, device=dev).to(torch.bfloat16)
             cache.append(0, k, v, total, p0)
             view = cache.view(0)
-            for n in (4, 16, 64):
+            for n in (4, 16, 128):
                 q = torch.randn((n, hq, d), generator=gen, device=dev).to(torch.bfloat16)
                 out = torch.empty_like(q)
 
@@ -750,9 +750,9 @@ def main() -> int:
                                          "unfused launch sequences"),
         "prefill_few_tokens": {
             "unit": "us per call", "points": few,
-            "workload": "32Q/8KV head_dim 128: n_new = 4 / 16 / 64 tokens after 8192 / 32768 "
+            "workload": "32Q/8KV head_dim 128: n_new = 4 / 16 / 128 tokens after 8192 / 32768 "
                         "cached keys; the flash prefill kernel vs AdaptiveAttention.run "
-                        "(split-K prefill over (token block, kv head) units for 2..64 tokens)"},
+                        "(split-K prefill over (token block, kv head) units for 2..128 tokens)"},
         "decode_step_unfused": {
             "value": round(dec["unfused_value"], 1), "unit": "GB/s",
             "ms_per_step": round(dec["unfused_ms_per_step"], 4),

@@ -167,7 +167,7 @@ int rth_attn_prefill(uint16_t* out, const uint16_t* q, const uint8_t* k,
  * rth_attn_prefill). partial: rth_split_scratch_floats(n_new * num_q_heads,
  * head_dim, num_splits) floats, no initialization needed. Shapes of the MFMA
  * decode kernel (rth_decode_path == RTH_DECODE_MFMA: head_dim 64 / 128 / 256,
- * groups of up to 16 q heads per block); 1 <= n_new <= 64. Results match
+ * groups of up to 16 q heads per block); 1 <= n_new <= 256. Results match
  * rth_attn_prefill within the attention tolerance (a different summation
  * order). */
 int rth_attn_prefill_split(uint16_t* out, const uint16_t* q, const uint8_t* k,

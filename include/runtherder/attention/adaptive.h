@@ -5,8 +5,9 @@
 // the reference's fixed 32. Calls of 2 .. kPrefillSplitTokens tokens on shapes
 // the MFMA decode kernel serves run rth_attn_prefill_split over the same
 // scratch with num_splits / (2 n_new) splits (no reference counterpart: a few
-// tokens after a long cache as split-K decode; 16 / 64 tokens after 8K keys
-// 209 / 199 -> 18 / 35 us per call, at an empty cache up to ~2 us slower).
+// tokens after a long cache as split-K decode; 16 / 64 / 128 tokens after 8K
+// keys 209 / 199 / 186 -> 18 / 35 / 57 us per call, at an empty cache up to
+// ~2.5 us slower).
 #pragma once
 
 #include <runtherder/attention/backend.h>
@@ -70,7 +71,7 @@ public:
 
     [[nodiscard]] int num_splits() const noexcept { return num_splits_; }
 
-    static constexpr int kPrefillSplitTokens = 64;
+    static constexpr int kPrefillSplitTokens = 128;
 
 private:
     AttnConfig                     config_;

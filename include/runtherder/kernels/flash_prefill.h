@@ -37,7 +37,7 @@ inline void flash_prefill_bf16(__hip_bfloat16*       out,
         stream));
 }
 
-// No reference counterpart: the same attention for 1 <= n_new <= 64 tokens
+// No reference counterpart: the same attention for 1 <= n_new <= 256 tokens
 // as split-K decode over (token block, kv head) units (rth_attn_prefill_split);
 // partial holds flash_split_scratch_floats(n_new * num_q_heads, head_dim,
 // num_splits) floats. head_dim 64 / 128 / 256.

@@ -144,7 +144,7 @@ int prefill_split_common(uint16_t* out, const uint16_t* q, const uint8_t* k, con
         return rc;
     }
     RTH_REQUIRE(partial != nullptr, "partial must not be null");
-    RTH_REQUIRE(n_new >= 1 && n_new <= rth::kPrefillSplitMaxTokens, "n_new must be in [1, 64]");
+    RTH_REQUIRE(n_new >= 1 && n_new <= rth::kPrefillSplitMaxTokens, "n_new must be in [1, 256]");
     RTH_REQUIRE(num_splits >= 1 && num_splits <= 65536, "num_splits must be in [1, 65536]");
     if (int rc = check_heads(num_q_heads, num_kv_heads)) {
         return rc;

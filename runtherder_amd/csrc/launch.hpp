@@ -64,7 +64,7 @@ hipError_t flash_decode_launch(uint16_t* out, const uint16_t* q,
 // K/V already in the cache) as split-K decode over n_new x Hkv virtual kv
 // heads: the shapes decode_mfma_supported accepts; partial holds
 // decode_scratch_floats(n_new * Hq, D, num_splits) floats.
-constexpr int kPrefillSplitMaxTokens = 64;
+constexpr int kPrefillSplitMaxTokens = 256;
 hipError_t flash_prefill_split_launch(uint16_t* out, const uint16_t* q, const uint8_t* k,
                                      const uint8_t* v, const float* k_scale,
                                      const float* v_scale, float* partial, int num_splits,

@@ -187,7 +187,7 @@ def flash_prefill_bf16(out, q, k, v, k_scale, v_scale, n_new, cache_len, num_q_h
               _stream(stream))
 
 
-PREFILL_SPLIT_MAX_TOKENS = 64
+PREFILL_SPLIT_MAX_TOKENS = 256
 
 
 def flash_prefill_split_bf16(out, q, k, v, k_scale, v_scale, partial, num_splits, n_new,
@@ -441,7 +441,7 @@ class AttentionBackend:
         raise NotImplementedError
 
 
-PREFILL_SPLIT_TOKENS = 64
+PREFILL_SPLIT_TOKENS = 128
 
 
 class AdaptiveAttention(AttentionBackend):
@@ -450,9 +450,9 @@ class AdaptiveAttention(AttentionBackend):
     device's (kv head, split) fill count. Calls of 2..PREFILL_SPLIT_TOKENS
     tokens on shapes the MFMA decode kernel serves take the split-K prefill
     (flash_prefill_split_bf16) over the same scratch, with num_splits //
-    (2 n_new) splits (no reference counterpart: per call, 16 / 64 tokens
-    after 8K keys 209 / 199 -> 18 / 35 us; at an empty cache up to ~2 us
-    slower)."""
+    (2 n_new) splits (no reference counterpart: per call, 16 / 64 / 128
+    tokens after 8K keys 209 / 199 / 186 -> 18 / 35 / 57 us; at an empty
+    cache up to ~2.5 us slower)."""
 
     def __init__(self, config: AttnConfig, num_splits: int | None = None, device="cuda"):
         self.config = config

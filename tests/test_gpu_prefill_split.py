@@ -52,7 +52,7 @@ CASES = [
     # 256 at 8 tokens per virtual head (its LDS staging row), a ragged last
     # token block.
     (37, 1500, 8, 8, 128, 16), (19, 700, 16, 8, 128, 32), (9, 900, 12, 2, 128, 64),
-    (20, 1234, 4, 4, 256, 16),
+    (20, 1234, 4, 4, 256, 16), (256, 3000, 32, 8, 128, 1), (128, 500, 24, 8, 64, 2),
 ]
 
 
@@ -126,22 +126,22 @@ def test_prefill_split_paged_equals_contiguous(total, n_new, block, splits):
 
 def test_prefill_split_rejects_bad_arguments():
     hq, hkv, d = 32, 8, 128
-    out = torch.empty((65, hq, d), dtype=torch.bfloat16, device=DEV)
+    out = torch.empty((257, hq, d), dtype=torch.bfloat16, device=DEV)
     q = torch.zeros_like(out)
     k = torch.zeros((100, hkv, d), dtype=torch.uint8, device=DEV)
     s = torch.zeros((100, hkv), dtype=torch.float32, device=DEV)
-    part = R.new_flash_split_scratch(65 * hq, d, 4)
+    part = R.new_flash_split_scratch(257 * hq, d, 4)
     with pytest.raises(R._ffi.RthError, match="n_new"):
-        R.flash_prefill_split_bf16(out, q, k, k, s, s, part, 4, 65, int_dev(0), hq, hkv, d, 0.1)
+        R.flash_prefill_split_bf16(out, q, k, k, s, s, part, 4, 257, int_dev(0), hq, hkv, d, 0.1)
     with pytest.raises(R._ffi.RthError, match="head_dim"):
         R.flash_prefill_split_bf16(out[:2, :, :32].contiguous(), q[:2, :, :32].contiguous(), k,
                                    k, s, s, part, 4, 2, int_dev(0), hq, hkv, 32, 0.1)
 
 
-@pytest.mark.parametrize("n_new", [2, 64, 65])
+@pytest.mark.parametrize("n_new", [2, 128, 129])
 def test_adaptive_backend_routes_small_prefill(n_new):
-    """AdaptiveAttention.run: 2..64 tokens take the split-K prefill over the
-    backend's scratch, 65 the flash prefill; both match the oracle."""
+    """AdaptiveAttention.run: 2..128 tokens take the split-K prefill over the
+    backend's scratch, 129 the flash prefill; both match the oracle."""
     hq, hkv, d, clen = 32, 8, 128, 3000
     scale = np.float32(1.0 / np.sqrt(d))
     q, k8, v8, ks, vs = inputs(n_new, clen, hq, hkv, d, 500 + n_new)
