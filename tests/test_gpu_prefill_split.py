@@ -155,3 +155,28 @@ def test_adaptive_backend_routes_small_prefill(n_new):
     want = O.attention_f32(q, k8, v8, ks, vs, n_new, clen, hq, hkv, d, scale, NTHREADS)
     mx, mean = O.bf16_err(bf16_host(out), want)
     assert mx <= MAX_ABS and mean <= MEAN_ABS, (mx, mean)
+
+
+def test_adaptive_backend_small_prefill_paged_equals_contiguous():
+    """The backend's few-token route on a paged view gives the contiguous
+    view's bytes (the same kernels through the block table)."""
+    hq, hkv, d, total, n_new, block = 32, 8, 128, 2100, 8, 64
+    clen = total - n_new
+    cont, paged, bt, table, _, _ = make_pair(total, hq, hkv, d, block, 90)
+    be = R.AdaptiveAttention(R.AttnConfig.for_heads(hq, hkv, d))
+    qh = O.normal_bf16((n_new, hq, d), 91)
+    q = bf16_dev(qh)
+    o1 = torch.empty((n_new, hq, d), dtype=torch.bfloat16, device=DEV)
+    o2 = torch.empty_like(o1)
+    step(f"adaptive paged few-token prefill total={total} n_new={n_new}")
+    be.run(o1, q, cont.view(0), n_new, int_dev(clen))
+    be.run(o2, q, paged.view(0, bt), n_new, int_dev(clen))
+    sync()
+    got = bf16_host(o2)
+    assert np.array_equal(bf16_host(o1), got)
+    gk, gv, gks, gvs = gather(paged, table, total, block)
+    want = O.attention_f32(qh, gk.reshape(total * hkv, d), gv.reshape(total * hkv, d),
+                           gks.reshape(-1), gvs.reshape(-1), n_new, clen, hq, hkv, d,
+                           np.float32(1.0 / np.sqrt(d)), NTHREADS)
+    mx, mean = O.bf16_err(got, want)
+    assert mx <= MAX_ABS and mean <= MEAN_ABS, (mx, mean)
