@@ -169,3 +169,18 @@ def test_fused_decode_steps_need_writable_slabs():
     slabs = R.KVSlabs(cache_k, cache_k, sc, sc)
     v2 = slabs.view()
     assert type(v2) is R.KVView and v2.k is cache_k and v2.block_table is None
+
+
+def test_prefill_split_rejects_bad_arguments():
+    def call(n_new=4, splits=8, hq=32, hkv=8, d=128, partial=FAKE, name="rth_attn_prefill_split"):
+        return _err(name, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, partial, splits, n_new, FAKE, hq,
+                    hkv, d, ctypes.c_float(0.1), None)
+    assert "n_new" in call(n_new=0)
+    assert "n_new" in call(n_new=257)
+    assert "num_splits" in call(splits=0)
+    assert "partial" in call(partial=None)
+    assert "divisible" in call(hq=30)
+    assert "MFMA" in call(d=32)
+    assert "power of two" in _err("rth_attn_prefill_split_paged", FAKE, FAKE, FAKE, FAKE, FAKE,
+                                  FAKE, FAKE, 48, FAKE, 8, 4, FAKE, 32, 8, 128,
+                                  ctypes.c_float(0.1), None)
