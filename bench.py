@@ -664,8 +664,9 @@ def main() -> int:
     ap.add_argument("--decode-kernel", choices=("auto", "valu"), default="auto",
                     help="valu: run every decode call on the VALU split kernel (A/B against "
                          "the MFMA kernel with --mode kernels or --sweep decode)")
-    ap.add_argument("--sweep", nargs="?", const="all", choices=("all", "decode", "prefill"),
-                    help="per-call decode and/or prefill sweeps over the BASELINE depths")
+    ap.add_argument("--sweep", nargs="?", const="all", choices=("all", "decode", "prefill", "few"),
+                    help="per-call decode and/or prefill sweeps over the BASELINE depths; few: "
+                         "the few-token prefill comparison alone")
     ap.add_argument("--mode", choices=("full", "kernels", "copy"), default="full",
                     help="kernels: eager launches of the bench kernels only (for "
                          "rocprofv3 --pmc); copy: a 256 MiB device copy (PMC "
@@ -688,6 +689,10 @@ def main() -> int:
         return copy_calibration(torch, stream)
     if args.mode == "kernels":
         return eager_kernels(torch, R, stream, args)
+    if args.sweep == "few":
+        for p in bench_few_token_prefill(torch, R, stream):
+            print(json.dumps({"prefill_few_tokens": p}), flush=True)
+        return 0
     if args.sweep:
         if args.sweep != "prefill":
             decode_kernel_sweep(torch, R, stream, [(24, 8, 35, None), (24, 8, 2041, None),
