@@ -377,7 +377,7 @@ def bench_few_token_prefill(torch, R, stream, iters=10):
     res = []
     be = R.AdaptiveAttention(R.AttnConfig.for_heads(hq, hkv, d))
     for clen in (8192, 32768):
-        total = clen + 128
+        total = clen + 512
         cache = R.KVCache(1, total, hkv, d, device=dev)
         p0 = torch.zeros(1, dtype=torch.int32, device=dev)
         cl = torch.full((1,), clen, dtype=torch.int32, device=dev)
@@ -401,6 +401,28 @@ def bench_few_token_prefill(torch, R, stream, iters=10):
                 au = graph_us(torch, stream, adaptive, iters)
                 res.append({"clen": clen, "n_new": n, "flash_prefill_us": round(fu, 2),
                             "adaptive_split_us": round(au, 2), "speedup": round(fu / au, 1)})
+            # Chunks beyond the backend's route through the entry itself:
+            # the flash prefill over key runs, about two rounds of workgroups.
+            cus = torch.cuda.get_device_properties(dev).multi_processor_count
+            for n in (256, 512):
+                q = torch.randn((n, hq, d), generator=gen, device=dev).to(torch.bfloat16)
+                out = torch.empty_like(q)
+                splits = max(1, min(16, 2 * cus // (((n + 127) // 128) * hq)))
+                part = R.new_flash_split_scratch(n * hq, d, splits, device=dev)
+
+                def flash():
+                    R.flash_prefill_bf16(out, q, view.k, view.v, view.k_scale, view.v_scale, n,
+                                         cl, hq, hkv, d, d ** -0.5)
+
+                def keysplit():
+                    R.flash_prefill_split_bf16(out, q, view.k, view.v, view.k_scale,
+                                               view.v_scale, part, splits, n, cl, hq, hkv, d,
+                                               d ** -0.5)
+                fu = graph_us(torch, stream, flash, iters)
+                su = graph_us(torch, stream, keysplit, iters)
+                res.append({"clen": clen, "n_new": n, "flash_prefill_us": round(fu, 2),
+                            "entry_key_runs_us": round(su, 2), "splits": splits,
+                            "speedup": round(fu / su, 1)})
         del cache
     return res
 
@@ -757,7 +779,9 @@ def main() -> int:
             "unit": "us per call", "points": few,
             "workload": "32Q/8KV head_dim 128: n_new = 4 / 16 / 128 tokens after 8192 / 32768 "
                         "cached keys; the flash prefill kernel vs AdaptiveAttention.run "
-                        "(split-K prefill over (token block, kv head) units for 2..128 tokens)"},
+                        "(split-K prefill over (token block, kv head) units for 2..128 tokens); "
+                        "256 / 512 tokens through rth_attn_prefill_split (the flash prefill over "
+                        "key runs, ~2 rounds of workgroups)"},
         "decode_step_unfused": {
             "value": round(dec["unfused_value"], 1), "unit": "GB/s",
             "ms_per_step": round(dec["unfused_ms_per_step"], 4),

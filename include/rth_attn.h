@@ -158,18 +158,20 @@ int rth_attn_prefill(uint16_t* out, const uint16_t* q, const uint8_t* k,
                      float scale, void* stream);
 
 /* No counterpart in the reference: the causal attention of rth_attn_prefill
- * for a few tokens after a long cache (speculative-decoding verification,
- * small prefill chunks), as split-K decode instead of one workgroup per q
- * tile streaming every key (reference flash_prefill.cu:34-241 walks all
- * keys serially per tile: n_new = 4 at 32K keys costs ~50x a decode step).
- * Every (token, kv head) is a decode unit over the first *cache_len + t + 1
- * keys; n_new tokens' K/V must already be in the cache (as for
- * rth_attn_prefill). partial: rth_split_scratch_floats(n_new * num_q_heads,
- * head_dim, num_splits) floats, no initialization needed. Shapes of the MFMA
- * decode kernel (rth_decode_path == RTH_DECODE_MFMA: head_dim 64 / 128 / 256,
- * groups of up to 16 q heads per block); 1 <= n_new <= 256. Results match
- * rth_attn_prefill within the attention tolerance (a different summation
- * order). */
+ * split over the keys, for calls after a long cache (speculative-decoding
+ * verification, prefill chunks), instead of one workgroup per q tile
+ * streaming every key (reference flash_prefill.cu:34-241 walks all keys
+ * serially per tile: n_new = 4 at 32K keys costs ~50x a decode step).
+ * n_new <= 128, or head_dim != 128: the decode split kernel over (block of
+ * tokens, kv head) units, token t over the first *cache_len + t + 1 keys
+ * (shapes of the MFMA decode kernel, rth_decode_path == RTH_DECODE_MFMA:
+ * head_dim 64 / 128 / 256; n_new <= 256). n_new > 128 at head_dim 128: the
+ * flash prefill with each (row block, q head) split over num_splits runs of
+ * key tiles. Both end in the decode merge. n_new's K/V must already be in the
+ * cache (as for rth_attn_prefill). partial: rth_split_scratch_floats(n_new *
+ * num_q_heads, head_dim, num_splits) floats, no initialization needed;
+ * 1 <= n_new <= 4096. Results match rth_attn_prefill within the attention
+ * tolerance (a different summation order). */
 int rth_attn_prefill_split(uint16_t* out, const uint16_t* q, const uint8_t* k,
                            const uint8_t* v, const float* k_scale, const float* v_scale,
                            float* partial, int num_splits, int n_new, const int* cache_len,

@@ -37,10 +37,11 @@ inline void flash_prefill_bf16(__hip_bfloat16*       out,
         stream));
 }
 
-// No reference counterpart: the same attention for 1 <= n_new <= 256 tokens
-// as split-K decode over (token block, kv head) units (rth_attn_prefill_split);
-// partial holds flash_split_scratch_floats(n_new * num_q_heads, head_dim,
-// num_splits) floats. head_dim 64 / 128 / 256.
+// No reference counterpart: the same attention split over the keys
+// (rth_attn_prefill_split): up to 128 tokens as split-K decode over (token
+// block, kv head) units, beyond as the flash prefill over num_splits key runs
+// per (row block, q head); partial holds flash_split_scratch_floats(n_new *
+// num_q_heads, head_dim, num_splits) floats.
 inline void flash_prefill_split_bf16(__hip_bfloat16*       out,
                                      const __hip_bfloat16* q,
                                      const __hip_fp8_e4m3* k,

@@ -144,11 +144,25 @@ int prefill_split_common(uint16_t* out, const uint16_t* q, const uint8_t* k, con
         return rc;
     }
     RTH_REQUIRE(partial != nullptr, "partial must not be null");
-    RTH_REQUIRE(n_new >= 1 && n_new <= rth::kPrefillSplitMaxTokens, "n_new must be in [1, 256]");
+    RTH_REQUIRE(n_new >= 1 && n_new <= rth::kPrefillSplitMaxTokens,
+                "n_new must be in [1, " + std::to_string(rth::kPrefillSplitMaxTokens) + "]");
     RTH_REQUIRE(num_splits >= 1 && num_splits <= 65536, "num_splits must be in [1, 65536]");
     if (int rc = check_heads(num_q_heads, num_kv_heads)) {
         return rc;
     }
+    // Up to kPrefillSplitDecodeTokens tokens (or at head_dim != 128, which the
+    // flash prefill does not serve): the decode split kernel over (token
+    // block, kv head) units; beyond, the flash prefill over key runs.
+    if (head_dim == 128 && n_new > rth::kPrefillSplitDecodeTokens) {
+        return check_hip(rth::flash_prefill_keysplit_launch(
+                             out, q, k, v, k_scale, v_scale, partial, num_splits, n_new, cache_len,
+                             num_q_heads, num_kv_heads, head_dim, scale, as_stream(stream),
+                             block_table, shift),
+                         what);
+    }
+    RTH_REQUIRE(n_new <= rth::kPrefillSplitDecodeMaxTokens,
+                "rth_attn_prefill_split: at head_dim != 128, n_new must be <= " +
+                    std::to_string(rth::kPrefillSplitDecodeMaxTokens));
     RTH_REQUIRE(rth::decode_mfma_supported(num_q_heads, num_kv_heads, head_dim),
                 "rth_attn_prefill_split: head_dim 64/128/256 with q-head groups the MFMA "
                 "decode kernel serves (rth_decode_path == RTH_DECODE_MFMA)");

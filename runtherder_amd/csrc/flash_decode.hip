@@ -2082,6 +2082,25 @@ hipError_t flash_prefill_split_launch(uint16_t* out, const uint16_t* q, const ui
     }
 }
 
+hipError_t split_rows_merge_launch(uint16_t* out, const float* partial, int num_splits,
+                                  const int* cache_len, int rows, int n_tok, int head_dim,
+                                  hipStream_t stream) {
+    switch (head_dim) {
+#define RTH_MERGE_CASE(DD)                                                                    \
+    case DD:                                                                                  \
+        hipLaunchKernelGGL((flash_decode_combine_kernel<DD, DD>),                            \
+                           dim3(static_cast<unsigned>(rows)), dim3(kCombineThreads), 0,      \
+                           stream, out, partial, num_splits, cache_len, rows, 0, 0, 0, n_tok); \
+        return hipGetLastError();
+        RTH_MERGE_CASE(64)
+        RTH_MERGE_CASE(128)
+        RTH_MERGE_CASE(256)
+#undef RTH_MERGE_CASE
+        default:
+            return hipErrorInvalidValue;
+    }
+}
+
 hipError_t flash_decode_valu_launch(uint16_t* out, const uint16_t* q, const uint8_t* k,
                                    const uint8_t* v, const float* k_scale,
                                    const float* v_scale, float* partial, int num_splits,

@@ -233,15 +233,23 @@ constexpr int waitcnt_vm(int n) {
 // go out together, so the prologue waits for one memory round trip instead of
 // three. Smaller grids, the key split and the 8-wave kernel keep the order
 // below (measured slower there, or spilling).
-template <int kWaves, bool kPaged, bool kSplit = false, bool kEarly = false>
+// kPart (4-wave workgroups): the keys are split over gridDim.y workgroups per
+// (row block, q head); workgroup y takes the y-th run of ceil(tiles / S) key
+// tiles and stores its rows' partials (m in log2 units, l, unnormalized O)
+// in the split-K decode layout ([rows, S] m, [rows, S] l, [rows, S, D] O,
+// rows t * Hq + h) for the decode merge; a row with no key in the run
+// stores m = -inf, l = 0, O = 0.
+template <int kWaves, bool kPaged, bool kSplit = false, bool kEarly = false, bool kPart = false>
 __global__ __launch_bounds__(kWaves * kWave, kSplit ? 1 : 2) void flash_prefill_kernel(
     uint16_t* __restrict__ out, const uint16_t* __restrict__ q,
     const uint8_t* __restrict__ k, const uint8_t* __restrict__ v,
     const float* __restrict__ ks, const float* __restrict__ vs, int n_new,
     const int* __restrict__ cache_len, int hq, int hkv, float scale_log2,
-    const int* __restrict__ block_table, int block_shift, bool one_round) {
+    const int* __restrict__ block_table, int block_shift, bool one_round,
+    float* __restrict__ partial, int num_splits) {
     static_assert(!kSplit || kWaves == 8, "the key split pairs two 4-wave halves");
     static_assert(!kEarly || (kWaves == 4 && !kSplit), "early issue: 4-wave workgroups only");
+    static_assert(!kPart || (kWaves == 4 && !kSplit && !kEarly), "key runs: 4-wave workgroups");
     constexpr int kThreads = kWaves * kWave;
     constexpr int kRowWaves = kSplit ? 4 : kWaves;  // waves with distinct rows
     constexpr int kBM      = 32 * kRowWaves;        // query rows per workgroup
@@ -292,10 +300,19 @@ __global__ __launch_bounds__(kWaves * kWave, kSplit ? 1 : 2) void flash_prefill_
     const int q0      = blk * kBM;
     const int last    = min(q0 + kBM, n_new) - 1;
     const int n_tiles = min((total + kBN - 1) / kBN, (clen + last) / kBN + 1);
+    // kPart: this workgroup's run of key tiles [kt_lo, kt_hi).
+    [[maybe_unused]] int kt_lo = 0;
+    [[maybe_unused]] int kt_hi = 0;
+    if constexpr (kPart) {
+        const int per = ((total + kBN - 1) / kBN + num_splits - 1) / num_splits;
+        kt_lo         = static_cast<int>(blockIdx.y) * per;
+        kt_hi         = min(kt_lo + per, n_tiles);
+    }
 
     // Key split: waves w and w + 4 hold the same rows; half g = w / 4 runs
     // the key tiles kt = g, g + 2, g + 4, ... and the halves merge at the end.
     const int split_g = kSplit ? (wave >> 2) : 0;
+    const int first_kt = kPart ? kt_lo : split_g;   // a wave's first tile
     const int wq0     = q0 + (kSplit ? (wave & 3) : wave) * 32;   // first row of this wave
     const int wlast   = min(wq0 + 31, n_new - 1);    // may be < wq0 (idle wave)
     const int w_tiles = (wlast < wq0) ? 0 : (clen + wlast) / kBN + 1;
@@ -510,7 +527,7 @@ __global__ __launch_bounds__(kWaves * kWave, kSplit ? 1 : 2) void flash_prefill_
             psum = (part[0] + part[1]) + (part[2] + part[3]);
         };
         exp_p();
-        if (__any((kt == split_g) || !(psum <= 0x1p15f))) {
+        if (__any((kt == first_kt) || !(psum <= 0x1p15f))) {
             float tmax = -INFINITY;
 #pragma unroll
             for (int kb = 0; kb < 2; ++kb) {
@@ -524,9 +541,9 @@ __global__ __launch_bounds__(kWaves * kWave, kSplit ? 1 : 2) void flash_prefill_
             // row that is here because another row of the wave overflowed may
             // sit far below its reference: lowering it would scale O and l by
             // 2^-tmax, which overflows.
-            const float delta = (kt == split_g) ? ((tmax == -INFINITY) ? 0.0f : tmax)
+            const float delta = (kt == first_kt) ? ((tmax == -INFINITY) ? 0.0f : tmax)
                                           : fmaxf(tmax, 0.0f);
-            const float alpha = (kt == split_g) ? 1.0f : __builtin_amdgcn_exp2f(-delta);
+            const float alpha = (kt == first_kt) ? 1.0f : __builtin_amdgcn_exp2f(-delta);
 #pragma unroll
             for (int kb = 0; kb < 2; ++kb) {
                 sx[kb] -= delta;
@@ -707,9 +724,10 @@ __global__ __launch_bounds__(kWaves * kWave, kSplit ? 1 : 2) void flash_prefill_
         // and V in raw1. (Tile "kt + 1" below is the stream's next tile,
         // kt + kStride.)
         VRaw<kReps> raw0, raw1;
+        const int t0 = kPart ? kt_lo : G;   // the stream's first tile
         {
-            const TileRows<kPaged> r0(G * kBN, total, block_table, block_shift);
-            const TileRows<kPaged> r1((G + kStride) * kBN, total, block_table, block_shift);
+            const TileRows<kPaged> r0(t0 * kBN, total, block_table, block_shift);
+            const TileRows<kPaged> r1((t0 + kStride) * kBN, total, block_table, block_shift);
             if constexpr (kEarly) {
                 raw0 = pre_raw0;
                 raw1 = pre_raw1;
@@ -726,8 +744,8 @@ __global__ __launch_bounds__(kWaves * kWave, kSplit ? 1 : 2) void flash_prefill_
 
         // Rows of the tiles one and two ahead, looked up (paged) a tile
         // before use.
-        TileRows<kPaged> rn1((G + kStride) * kBN, total, block_table, block_shift);
-        TileRows<kPaged> rn2((G + 2 * kStride) * kBN, total, block_table, block_shift);
+        TileRows<kPaged> rn1((t0 + kStride) * kBN, total, block_table, block_shift);
+        TileRows<kPaged> rn2((t0 + 2 * kStride) * kBN, total, block_table, block_shift);
         // One tile from buffer B (static, so each buffer is a distinct array).
         auto tile = [&]<int B>(int kt) {
             uint8_t*  kb0 = G ? sK2 : sK0;
@@ -825,11 +843,11 @@ __global__ __launch_bounds__(kWaves * kWave, kSplit ? 1 : 2) void flash_prefill_
             lds_barrier();
         };
 
-        const int n_steps = (n_tiles + kStride - 1) / kStride;
+        const int n_steps = kPart ? kt_hi - kt_lo : (n_tiles + kStride - 1) / kStride;
         for (int i = 0; i < n_steps; i += 2) {
-            tile.template operator()<0>(G + kStride * i);
+            tile.template operator()<0>(t0 + kStride * i);
             if (i + 1 < n_steps) {
-                tile.template operator()<1>(G + kStride * (i + 1));
+                tile.template operator()<1>(t0 + kStride * (i + 1));
             }
         }
     };
@@ -888,6 +906,30 @@ __global__ __launch_bounds__(kWaves * kWave, kSplit ? 1 : 2) void flash_prefill_
     }
 
     const float l_tot = wave_xor_sum(l_run, 32);
+    if constexpr (kPart) {
+        if (my_q < n_new) {
+            const int64_t rows   = static_cast<int64_t>(n_new) * hq;
+            const int64_t slot   = (static_cast<int64_t>(my_q) * hq + qh) * num_splits +
+                                 static_cast<int64_t>(blockIdx.y);
+            const bool    any    = l_tot > 0.0f;
+            float*        part_o = partial + 2 * rows * num_splits + slot * kHD;
+            if (h == 0) {
+                partial[slot]                     = any ? m_ref : -INFINITY;
+                partial[rows * num_splits + slot] = l_tot;
+            }
+#pragma unroll
+            for (int db = 0; db < 4; ++db) {
+#pragma unroll
+                for (int rg = 0; rg < 4; ++rg) {
+                    *reinterpret_cast<f32x4*>(part_o + 32 * db + 8 * rg + 4 * h) =
+                        any ? f32x4{o[db][4 * rg], o[db][4 * rg + 1], o[db][4 * rg + 2],
+                                    o[db][4 * rg + 3]}
+                            : f32x4{0.f, 0.f, 0.f, 0.f};
+                }
+            }
+        }
+        return;
+    }
     if (my_q < n_new) {
         const float inv_l = 1.0f / l_tot;
         uint16_t*   orow  = out + (static_cast<int64_t>(my_q) * hq + qh) * kHD;
@@ -922,27 +964,72 @@ void launch_prefill(uint16_t* out, const uint16_t* q, const uint8_t* k, const ui
             hipLaunchKernelGGL((flash_prefill_kernel<kWaves, true, kSplit, kEarlyOk>), grid,
                                dim3(kWaves * kWave), 0, stream, out, q, k, v, k_scale, v_scale,
                                n_new, cache_len, hq, hkv, scale_log2, block_table, block_shift,
-                               one_round);
+                               one_round, nullptr, 1);
         } else {
             hipLaunchKernelGGL((flash_prefill_kernel<kWaves, true, kSplit>), grid,
                                dim3(kWaves * kWave), 0, stream, out, q, k, v, k_scale, v_scale,
                                n_new, cache_len, hq, hkv, scale_log2, block_table, block_shift,
-                               one_round);
+                               one_round, nullptr, 1);
         }
     } else {
         if (early) {
             hipLaunchKernelGGL((flash_prefill_kernel<kWaves, false, kSplit, kEarlyOk>), grid,
                                dim3(kWaves * kWave), 0, stream, out, q, k, v, k_scale, v_scale,
-                               n_new, cache_len, hq, hkv, scale_log2, nullptr, 0, one_round);
+                               n_new, cache_len, hq, hkv, scale_log2, nullptr, 0, one_round,
+                               nullptr, 1);
         } else {
             hipLaunchKernelGGL((flash_prefill_kernel<kWaves, false, kSplit>), grid,
                                dim3(kWaves * kWave), 0, stream, out, q, k, v, k_scale, v_scale,
-                               n_new, cache_len, hq, hkv, scale_log2, nullptr, 0, one_round);
+                               n_new, cache_len, hq, hkv, scale_log2, nullptr, 0, one_round,
+                               nullptr, 1);
         }
     }
 }
 
+// The flash prefill with its keys split over num_splits workgroups per (row
+// block, q head), then the decode merge over the n_new * Hq rows.
+template <bool kPaged>
+hipError_t launch_prefill_part(uint16_t* out, const uint16_t* q, const uint8_t* k,
+                               const uint8_t* v, const float* k_scale, const float* v_scale,
+                               float* partial, int num_splits, int n_new, const int* cache_len,
+                               int hq, int hkv, float scale_log2, hipStream_t stream,
+                               const int* block_table, int block_shift) {
+    constexpr int kBM   = 32 * 4;
+    const int     n_blk = (n_new + kBM - 1) / kBM;
+    const dim3    grid(static_cast<unsigned>(n_blk * hq), static_cast<unsigned>(num_splits));
+    hipLaunchKernelGGL((flash_prefill_kernel<4, kPaged, false, false, true>), grid,
+                       dim3(4 * kWave), 0, stream, out, q, k, v, k_scale, v_scale, n_new,
+                       cache_len, hq, hkv, scale_log2, block_table, block_shift, false, partial,
+                       num_splits);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) {
+        return e;
+    }
+    return split_rows_merge_launch(out, partial, num_splits, cache_len, n_new * hq, n_new, kHD,
+                                   stream);
+}
+
 }  // namespace
+
+hipError_t flash_prefill_keysplit_launch(uint16_t* out, const uint16_t* q, const uint8_t* k,
+                                         const uint8_t* v, const float* k_scale,
+                                         const float* v_scale, float* partial, int num_splits,
+                                         int n_new, const int* cache_len, int num_q_heads,
+                                         int num_kv_heads, int head_dim, float scale,
+                                         hipStream_t stream, const int* block_table,
+                                         int block_shift) {
+    if (head_dim != kHD) {
+        return hipErrorInvalidValue;
+    }
+    const float sl = scale * kLog2e;
+    return block_table != nullptr
+               ? launch_prefill_part<true>(out, q, k, v, k_scale, v_scale, partial, num_splits,
+                                           n_new, cache_len, num_q_heads, num_kv_heads, sl,
+                                           stream, block_table, block_shift)
+               : launch_prefill_part<false>(out, q, k, v, k_scale, v_scale, partial, num_splits,
+                                            n_new, cache_len, num_q_heads, num_kv_heads, sl,
+                                            stream, nullptr, 0);
+}
 
 hipError_t flash_prefill_launch(uint16_t* out, const uint16_t* q,
                                 const uint8_t* k, const uint8_t* v,

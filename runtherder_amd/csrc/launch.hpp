@@ -64,7 +64,9 @@ hipError_t flash_decode_launch(uint16_t* out, const uint16_t* q,
 // K/V already in the cache) as split-K decode over n_new x Hkv virtual kv
 // heads: the shapes decode_mfma_supported accepts; partial holds
 // decode_scratch_floats(n_new * Hq, D, num_splits) floats.
-constexpr int kPrefillSplitMaxTokens = 256;
+constexpr int kPrefillSplitMaxTokens       = 4096;   // rth_attn_prefill_split
+constexpr int kPrefillSplitDecodeTokens    = 128;    // above: the flash prefill over key runs
+constexpr int kPrefillSplitDecodeMaxTokens = 256;    // the decode kernel's route at D != 128
 hipError_t flash_prefill_split_launch(uint16_t* out, const uint16_t* q, const uint8_t* k,
                                      const uint8_t* v, const float* k_scale,
                                      const float* v_scale, float* partial, int num_splits,
@@ -72,6 +74,25 @@ hipError_t flash_prefill_split_launch(uint16_t* out, const uint16_t* q, const ui
                                      int num_kv_heads, int head_dim, float scale,
                                      hipStream_t stream, const int* block_table = nullptr,
                                      int block_shift = 0);
+
+// The decode merge over `rows` rows of num_splits partials each (whole-row
+// workgroups): out row r = the merged row r; the live slots follow from
+// *cache_len + n_tok keys as in the split kernels.
+hipError_t split_rows_merge_launch(uint16_t* out, const float* partial, int num_splits,
+                                  const int* cache_len, int rows, int n_tok, int head_dim,
+                                  hipStream_t stream);
+
+// The flash prefill (head_dim 128) with its keys split over num_splits
+// workgroups per (128-row block, q head), partials in the split-K decode
+// layout (decode_scratch_floats(n_new * Hq, 128, num_splits) floats), then
+// split_rows_merge_launch.
+hipError_t flash_prefill_keysplit_launch(uint16_t* out, const uint16_t* q, const uint8_t* k,
+                                         const uint8_t* v, const float* k_scale,
+                                         const float* v_scale, float* partial, int num_splits,
+                                         int n_new, const int* cache_len, int num_q_heads,
+                                         int num_kv_heads, int head_dim, float scale,
+                                         hipStream_t stream, const int* block_table = nullptr,
+                                         int block_shift = 0);
 
 // The VALU split kernel + merge: head_dim in {32, 64, 128, 256, 512}, any
 // GQA group (no paging, no fused append). The decode entry points use it for

@@ -187,16 +187,18 @@ def flash_prefill_bf16(out, q, k, v, k_scale, v_scale, n_new, cache_len, num_q_h
               _stream(stream))
 
 
-PREFILL_SPLIT_MAX_TOKENS = 256
+PREFILL_SPLIT_MAX_TOKENS = 4096
 
 
 def flash_prefill_split_bf16(out, q, k, v, k_scale, v_scale, partial, num_splits, n_new,
                              cache_len, num_q_heads, num_kv_heads, head_dim, scale,
                              stream=None):
-    """flash_prefill_bf16 for a few tokens after a long cache, as split-K
-    decode over (token, kv head) units (no reference counterpart; the
-    reference walks every key serially per q tile, flash_prefill.cu:34-241).
-    partial: flash_split_scratch_floats(n_new * num_q_heads, head_dim,
+    """flash_prefill_bf16 split over the keys, for calls after a long cache
+    (no reference counterpart; the reference walks every key serially per q
+    tile, flash_prefill.cu:34-241): up to 128 tokens as split-K decode over
+    (token block, kv head) units, beyond (head_dim 128) the flash prefill over
+    num_splits key runs per (row block, q head), both merged by the decode
+    merge. partial: flash_split_scratch_floats(n_new * num_q_heads, head_dim,
     num_splits) floats; 1 <= n_new <= PREFILL_SPLIT_MAX_TOKENS."""
     _need(out, torch.bfloat16, "out"); _need(q, torch.bfloat16, "q")
     _need(k, torch.uint8, "k"); _need(v, torch.uint8, "v")

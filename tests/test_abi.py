@@ -176,7 +176,8 @@ def test_prefill_split_rejects_bad_arguments():
         return _err(name, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, partial, splits, n_new, FAKE, hq,
                     hkv, d, ctypes.c_float(0.1), None)
     assert "n_new" in call(n_new=0)
-    assert "n_new" in call(n_new=257)
+    assert "n_new" in call(n_new=4097)
+    assert "<= 256" in call(n_new=300, d=256)
     assert "num_splits" in call(splits=0)
     assert "partial" in call(partial=None)
     assert "divisible" in call(hq=30)

@@ -52,7 +52,11 @@ CASES = [
     # 256 at 8 tokens per virtual head (its LDS staging row), a ragged last
     # token block.
     (37, 1500, 8, 8, 128, 16), (19, 700, 16, 8, 128, 32), (9, 900, 12, 2, 128, 64),
-    (20, 1234, 4, 4, 256, 16), (256, 3000, 32, 8, 128, 1), (128, 500, 24, 8, 64, 2),
+    (20, 1234, 4, 4, 256, 16), (256, 3000, 24, 4, 64, 1), (128, 500, 24, 8, 64, 2),
+    # beyond 64 tokens at head_dim 128: the flash prefill over key runs (runs
+    # past the cache, more runs than tiles, one run, ragged row blocks).
+    (100, 3000, 32, 8, 128, 4), (300, 5000, 24, 8, 128, 8), (1000, 200, 32, 8, 128, 3),
+    (129, 0, 8, 1, 128, 16), (517, 7777, 16, 4, 128, 5), (256, 3000, 32, 8, 128, 1),
 ]
 
 
@@ -91,7 +95,7 @@ def test_prefill_split_single_token_equals_decode():
 
 
 @pytest.mark.parametrize("total,n_new,block,splits", [(1500, 4, 64, 32), (3000, 16, 32, 16),
-                                                      (777, 9, 256, 64)])
+                                                      (777, 9, 256, 64), (3000, 200, 64, 4)])
 def test_prefill_split_paged_equals_contiguous(total, n_new, block, splits):
     hq, hkv, d = 32, 8, 128
     clen = total - n_new
@@ -126,13 +130,13 @@ def test_prefill_split_paged_equals_contiguous(total, n_new, block, splits):
 
 def test_prefill_split_rejects_bad_arguments():
     hq, hkv, d = 32, 8, 128
-    out = torch.empty((257, hq, d), dtype=torch.bfloat16, device=DEV)
+    out = torch.empty((4097, hq, d), dtype=torch.bfloat16, device=DEV)
     q = torch.zeros_like(out)
     k = torch.zeros((100, hkv, d), dtype=torch.uint8, device=DEV)
     s = torch.zeros((100, hkv), dtype=torch.float32, device=DEV)
-    part = R.new_flash_split_scratch(257 * hq, d, 4)
+    part = R.new_flash_split_scratch(2 * hq, d, 4)
     with pytest.raises(R._ffi.RthError, match="n_new"):
-        R.flash_prefill_split_bf16(out, q, k, k, s, s, part, 4, 257, int_dev(0), hq, hkv, d, 0.1)
+        R.flash_prefill_split_bf16(out, q, k, k, s, s, part, 4, 4097, int_dev(0), hq, hkv, d, 0.1)
     with pytest.raises(R._ffi.RthError, match="head_dim"):
         R.flash_prefill_split_bf16(out[:2, :, :32].contiguous(), q[:2, :, :32].contiguous(), k,
                                    k, s, s, part, 4, 2, int_dev(0), hq, hkv, 32, 0.1)
