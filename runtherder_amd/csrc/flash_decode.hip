@@ -1451,7 +1451,8 @@ __device__ __forceinline__ float quad_group_sum(float v) {
 template <int D, int kSlice = kCombineSlice>
 __global__ __launch_bounds__(kCombineThreads) void flash_decode_combine_kernel(
     uint16_t* __restrict__ out, const float* __restrict__ partial, int num_splits,
-    const int* __restrict__ cache_len, int hq, int kvg, int xl_g, int append, int n_tok) {
+    const int* __restrict__ cache_len, int hq, int kvg, int xl_g, int append, int n_tok,
+    int run_min = 0) {
     static_assert(D % kSlice == 0, "slices tile the row");
     constexpr int kQuads  = kSlice / 4;
     constexpr int kGroups = kCombineThreads / kQuads;
@@ -1512,9 +1513,14 @@ __global__ __launch_bounds__(kCombineThreads) void flash_decode_combine_kernel(
     // Live slots: as the split kernel derives them (an append call's key may
     // hold a slot of its own).
     const int cache_t = (n_keys + kTileKeys - 2) / kTileKeys;
-    const int n_eff   = (append != 0 && cache_t <= 2 * (num_splits - 1))
+    int       n_eff   = (append != 0 && cache_t <= 2 * (num_splits - 1))
                             ? min(num_splits - 1, cache_t) + 1
                             : dec_partition(n_keys, num_splits, kvg).n_eff;
+    if (kSlice == D && run_min > 0) {   // the flash prefill's key runs (64-key tiles)
+        const int tiles = (n_keys + 63) / 64;
+        const int per   = max((tiles + num_splits - 1) / num_splits, run_min);
+        n_eff           = (tiles + per - 1) / per;
+    }
     float     M       = -INFINITY;
     for (int s0 = 0;; s0 += 4 * kWave) {
 #pragma unroll
@@ -1542,7 +1548,9 @@ __global__ __launch_bounds__(kCombineThreads) void flash_decode_combine_kernel(
         for (int u = 0; u < 8; ++u) {
             const bool  live = s0 + u * kGroups < n_eff;
             const float f    = live ? __builtin_amdgcn_exp2f(ms[u] - M) : 0.0f;
-            const f32x4 o    = live ? os[u] : f32x4{0.f, 0.f, 0.f, 0.f};
+            // Whole-row merges: a slot with m = -inf may hold no O at all.
+            const bool  use  = kSlice == D ? (live && ms[u] != -INFINITY) : live;
+            const f32x4 o    = use ? os[u] : f32x4{0.f, 0.f, 0.f, 0.f};
             acc += o * f;
             l += (live ? ls[u] : 0.0f) * f;
         }
@@ -2084,13 +2092,14 @@ hipError_t flash_prefill_split_launch(uint16_t* out, const uint16_t* q, const ui
 
 hipError_t split_rows_merge_launch(uint16_t* out, const float* partial, int num_splits,
                                   const int* cache_len, int rows, int n_tok, int head_dim,
-                                  hipStream_t stream) {
+                                  hipStream_t stream, int run_min) {
     switch (head_dim) {
 #define RTH_MERGE_CASE(DD)                                                                    \
     case DD:                                                                                  \
         hipLaunchKernelGGL((flash_decode_combine_kernel<DD, DD>),                            \
                            dim3(static_cast<unsigned>(rows)), dim3(kCombineThreads), 0,      \
-                           stream, out, partial, num_splits, cache_len, rows, 0, 0, 0, n_tok); \
+                           stream, out, partial, num_splits, cache_len, rows, 0, 0, 0, n_tok,  \
+                           run_min);                                                           \
         return hipGetLastError();
         RTH_MERGE_CASE(64)
         RTH_MERGE_CASE(128)

@@ -234,11 +234,14 @@ constexpr int waitcnt_vm(int n) {
 // three. Smaller grids, the key split and the 8-wave kernel keep the order
 // below (measured slower there, or spilling).
 // kPart (4-wave workgroups): the keys are split over gridDim.y workgroups per
-// (row block, q head); workgroup y takes the y-th run of ceil(tiles / S) key
-// tiles and stores its rows' partials (m in log2 units, l, unnormalized O)
-// in the split-K decode layout ([rows, S] m, [rows, S] l, [rows, S, D] O,
-// rows t * Hq + h) for the decode merge; a row with no key in the run
-// stores m = -inf, l = 0, O = 0.
+// (row block, q head); workgroup y takes the y-th run of
+// max(ceil(tiles / S), kPartMinTiles) key tiles and stores its rows'
+// partials (m in log2 units, l, unnormalized O) in the split-K decode layout
+// ([rows, S] m, [rows, S] l, [rows, S, D] O, rows t * Hq + h) for the decode
+// merge; a row with no key in the run stores m = -inf, l = 0 and, in a
+// workgroup that has keys, O = 0 (a workgroup without keys leaves O unwritten;
+// the merge drops slots with m = -inf).
+constexpr int kPartMinTiles = 8;   // a run's minimum: short caches use few runs
 template <int kWaves, bool kPaged, bool kSplit = false, bool kEarly = false, bool kPart = false>
 __global__ __launch_bounds__(kWaves * kWave, kSplit ? 1 : 2) void flash_prefill_kernel(
     uint16_t* __restrict__ out, const uint16_t* __restrict__ q,
@@ -304,9 +307,21 @@ __global__ __launch_bounds__(kWaves * kWave, kSplit ? 1 : 2) void flash_prefill_
     [[maybe_unused]] int kt_lo = 0;
     [[maybe_unused]] int kt_hi = 0;
     if constexpr (kPart) {
-        const int per = ((total + kBN - 1) / kBN + num_splits - 1) / num_splits;
+        const int per = max(((total + kBN - 1) / kBN + num_splits - 1) / num_splits,
+                            kPartMinTiles);
         kt_lo         = static_cast<int>(blockIdx.y) * per;
         kt_hi         = min(kt_lo + per, n_tiles);
+        if (kt_hi <= kt_lo) {   // no key of this run for any row of the block: m, l only
+            const int r = q0 + tid;
+            if (tid < kBM && r < n_new) {
+                const int64_t rows = static_cast<int64_t>(n_new) * hq;
+                const int64_t slot = (static_cast<int64_t>(r) * hq + qh) * num_splits +
+                                     static_cast<int64_t>(blockIdx.y);
+                partial[slot]                     = -INFINITY;
+                partial[rows * num_splits + slot] = 0.0f;
+            }
+            return;
+        }
     }
 
     // Key split: waves w and w + 4 hold the same rows; half g = w / 4 runs
@@ -1006,7 +1021,7 @@ hipError_t launch_prefill_part(uint16_t* out, const uint16_t* q, const uint8_t* 
         return e;
     }
     return split_rows_merge_launch(out, partial, num_splits, cache_len, n_new * hq, n_new, kHD,
-                                   stream);
+                                   stream, kPartMinTiles);
 }
 
 }  // namespace

@@ -77,10 +77,11 @@ hipError_t flash_prefill_split_launch(uint16_t* out, const uint16_t* q, const ui
 
 // The decode merge over `rows` rows of num_splits partials each (whole-row
 // workgroups): out row r = the merged row r; the live slots follow from
-// *cache_len + n_tok keys as in the split kernels.
+// *cache_len + n_tok keys as in the split kernels, or (run_min > 0) as the
+// flash prefill's key runs of max(ceil(tiles / S), run_min) 64-key tiles.
 hipError_t split_rows_merge_launch(uint16_t* out, const float* partial, int num_splits,
                                   const int* cache_len, int rows, int n_tok, int head_dim,
-                                  hipStream_t stream);
+                                  hipStream_t stream, int run_min = 0);
 
 // The flash prefill (head_dim 128) with its keys split over num_splits
 // workgroups per (128-row block, q head), partials in the split-K decode
