@@ -368,7 +368,7 @@ def bench_few_token_prefill(torch, R, stream, iters=10):
     """A causal prefill call of a few tokens after a long cache (32Q/8KV,
     head_dim 128): the flash prefill kernel (rth_attn_prefill, one workgroup
     per q tile walking every key, as the reference's) against
-    AdaptiveAttention.run, which routes 2..128 tokens to the split-K prefill
+    AdaptiveAttention.run, which routes 2..256 tokens to the split-K prefill
     over its scratch (rth_attn_prefill_split)."""
     hq, hkv, d = 32, 8, 128
     dev = torch.device("cuda:0")
@@ -387,7 +387,7 @@ def bench_few_token_prefill(torch, R, stream, iters=10):
             v = torch.randn((total, hkv, d), generator=gen, device=dev).to(torch.bfloat16)
             cache.append(0, k, v, total, p0)
             view = cache.view(0)
-            for n in (4, 16, 128):
+            for n in (4, 16, 128, 256):
                 q = torch.randn((n, hq, d), generator=gen, device=dev).to(torch.bfloat16)
                 out = torch.empty_like(q)
 
@@ -401,10 +401,10 @@ def bench_few_token_prefill(torch, R, stream, iters=10):
                 au = graph_us(torch, stream, adaptive, iters)
                 res.append({"clen": clen, "n_new": n, "flash_prefill_us": round(fu, 2),
                             "adaptive_split_us": round(au, 2), "speedup": round(fu / au, 1)})
-            # Chunks beyond the backend's route through the entry itself:
+            # A chunk beyond the backend's routes through the entry itself:
             # the flash prefill over key runs, about two rounds of workgroups.
             cus = torch.cuda.get_device_properties(dev).multi_processor_count
-            for n in (256, 512):
+            for n in (512,):
                 q = torch.randn((n, hq, d), generator=gen, device=dev).to(torch.bfloat16)
                 out = torch.empty_like(q)
                 splits = max(1, min(16, 2 * cus // (((n + 127) // 128) * hq)))
@@ -777,11 +777,11 @@ def main() -> int:
                                          "unfused launch sequences"),
         "prefill_few_tokens": {
             "unit": "us per call", "points": few,
-            "workload": "32Q/8KV head_dim 128: n_new = 4 / 16 / 128 tokens after 8192 / 32768 "
+            "workload": "32Q/8KV head_dim 128: n_new = 4 / 16 / 128 / 256 / 512 tokens after 8192 / 32768 "
                         "cached keys; the flash prefill kernel vs AdaptiveAttention.run "
-                        "(split-K prefill over (token block, kv head) units for 2..128 tokens); "
-                        "256 / 512 tokens through rth_attn_prefill_split (the flash prefill over "
-                        "key runs, ~2 rounds of workgroups)"},
+                        "(split-K decode over (token block, kv head) units for 2..128 tokens, the "
+                        "flash prefill over key runs for 129..256); 512 tokens through "
+                        "rth_attn_prefill_split (key runs, ~2 rounds of workgroups)"},
         "decode_step_unfused": {
             "value": round(dec["unfused_value"], 1), "unit": "GB/s",
             "ms_per_step": round(dec["unfused_ms_per_step"], 4),

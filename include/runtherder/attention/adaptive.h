@@ -7,7 +7,10 @@
 // scratch with num_splits / (2 n_new) splits (no reference counterpart: a few
 // tokens after a long cache as split-K decode; 16 / 64 / 128 tokens after 8K
 // keys 209 / 199 / 186 -> 18 / 35 / 57 us per call, at an empty cache up to
-// ~2.5 us slower).
+// ~2.5 us slower), and at head_dim 128 calls of up to kPrefillRunsTokens
+// tokens run it as the flash prefill over key runs (256 tokens after 8K / 32K
+// keys 186 / 830 -> 67 / 179 us; at an empty cache 14 -> 27 us). For those
+// the scratch holds kPrefillRunTokenRuns token-runs (34 MB at 32 q heads).
 #pragma once
 
 #include <runtherder/attention/backend.h>
@@ -71,11 +74,18 @@ public:
 
     [[nodiscard]] int num_splits() const noexcept { return num_splits_; }
 
-    static constexpr int kPrefillSplitTokens = 128;
+    static constexpr int kPrefillSplitTokens  = 128;
+    static constexpr int kPrefillRunsTokens   = 256;
+    static constexpr int kPrefillRunTokenRuns = 2048;
 
 private:
+    // Split count of rth_attn_prefill_split for an n_new-token call, 0 when
+    // the call takes the flash prefill (or decode) instead.
+    [[nodiscard]] int prefill_split_count(int n_new) const noexcept;
+
     AttnConfig                     config_;
     int                            num_splits_;
+    int                            cus_ = 256;
     device::DeviceUniquePtr<float> partial_;  // split decode reduction scratch
 };
 

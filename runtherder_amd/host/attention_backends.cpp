@@ -30,8 +30,33 @@ AdaptiveAttention::AdaptiveAttention(const AttnConfig& config)
 AdaptiveAttention::AdaptiveAttention(const AttnConfig& config, int num_splits)
     : config_(config), num_splits_(num_splits) {
     RUNTHERDER_CHECK(num_splits >= 1, "AdaptiveAttention num_splits must be >= 1");
-    partial_ = device::make_device_unique<float>(
-        rth_split_scratch_floats(config.num_q_heads, config.head_dim, num_splits));
+    int dev = 0;
+    RUNTHERDER_HIP_CHECK(hipGetDevice(&dev));
+    RUNTHERDER_HIP_CHECK(hipDeviceGetAttribute(&cus_, hipDeviceAttributeMultiprocessorCount, dev));
+    const std::size_t dec =
+        rth_split_scratch_floats(config.num_q_heads, config.head_dim, num_splits);
+    const std::size_t runs =
+        config.head_dim == 128
+            ? rth_split_scratch_floats(config.num_q_heads, config.head_dim, kPrefillRunTokenRuns)
+            : 0;
+    partial_ = device::make_device_unique<float>(dec > runs ? dec : runs);
+}
+
+int AdaptiveAttention::prefill_split_count(int n_new) const noexcept {
+    if (n_new >= 2 && n_new <= kPrefillSplitTokens &&
+        rth_decode_path(config_.num_q_heads, config_.num_kv_heads, config_.head_dim) ==
+            RTH_DECODE_MFMA) {
+        return num_splits_ / (2 * n_new) > 1 ? num_splits_ / (2 * n_new) : 1;
+    }
+    if (n_new > kPrefillSplitTokens && n_new <= kPrefillRunsTokens && config_.head_dim == 128) {
+        // About two rounds of 4-wave workgroups, within the scratch.
+        const int blocks = (n_new + 127) / 128 * config_.num_q_heads;
+        int       runs   = 2 * cus_ / blocks;
+        runs             = runs < 16 ? runs : 16;
+        runs             = runs < kPrefillRunTokenRuns / n_new ? runs : kPrefillRunTokenRuns / n_new;
+        return runs > 1 ? runs : 0;
+    }
+    return 0;
 }
 
 void AdaptiveAttention::run(__hip_bfloat16* out, const __hip_bfloat16* q, const KVView& kv,
@@ -41,10 +66,7 @@ void AdaptiveAttention::run(__hip_bfloat16* out, const __hip_bfloat16* q, const 
     auto* k  = reinterpret_cast<const std::uint8_t*>(kv.k);
     auto* v  = reinterpret_cast<const std::uint8_t*>(kv.v);
     const bool paged = kv.block_table != nullptr;
-    if (n_new >= 2 && n_new <= kPrefillSplitTokens &&
-        rth_decode_path(config_.num_q_heads, config_.num_kv_heads, config_.head_dim) ==
-            RTH_DECODE_MFMA) {
-        const int splits = num_splits_ / (2 * n_new) > 1 ? num_splits_ / (2 * n_new) : 1;
+    if (const int splits = prefill_split_count(n_new); splits > 0) {
         if (paged) {
             RUNTHERDER_RTH_CHECK(rth_attn_prefill_split_paged(
                 o, qq, k, v, kv.k_scale, kv.v_scale, kv.block_table, kv.block_size,

@@ -444,6 +444,8 @@ class AttentionBackend:
 
 
 PREFILL_SPLIT_TOKENS = 128
+PREFILL_RUNS_TOKENS = 256
+PREFILL_RUN_TOKEN_RUNS = 2048
 
 
 class AdaptiveAttention(AttentionBackend):
@@ -454,22 +456,33 @@ class AdaptiveAttention(AttentionBackend):
     (flash_prefill_split_bf16) over the same scratch, with num_splits //
     (2 n_new) splits (no reference counterpart: per call, 16 / 64 / 128
     tokens after 8K keys 209 / 199 / 186 -> 18 / 35 / 57 us; at an empty
-    cache up to ~2.5 us slower)."""
+    cache up to ~2.5 us slower); at head_dim 128, calls of up to
+    PREFILL_RUNS_TOKENS tokens take it as the flash prefill over key runs
+    (256 tokens after 8K / 32K keys 186 / 830 -> 67 / 179 us; at an empty
+    cache 14 -> 27 us), for which the scratch holds PREFILL_RUN_TOKEN_RUNS
+    token-runs."""
 
     def __init__(self, config: AttnConfig, num_splits: int | None = None, device="cuda"):
         self.config = config
         self.num_splits = num_splits or default_num_splits(
             config.num_kv_heads, torch.device(device).index or 0)
+        dev = torch.device(device)
+        self.cus = torch.cuda.get_device_properties(dev).multi_processor_count
+        runs = PREFILL_RUN_TOKEN_RUNS if config.head_dim == 128 else 1
         self.partial = new_flash_split_scratch(config.num_q_heads, config.head_dim,
-                                               self.num_splits, device=device)
+                                               max(self.num_splits, runs), device=device)
 
     def _split_prefill_splits(self, n_new):
         c = self.config
-        if not 2 <= n_new <= PREFILL_SPLIT_TOKENS:
-            return 0
-        if decode_path(c.num_q_heads, c.num_kv_heads, c.head_dim) != DECODE_MFMA:
-            return 0
-        return max(1, self.num_splits // (2 * n_new))
+        if 2 <= n_new <= PREFILL_SPLIT_TOKENS:
+            if decode_path(c.num_q_heads, c.num_kv_heads, c.head_dim) != DECODE_MFMA:
+                return 0
+            return max(1, self.num_splits // (2 * n_new))
+        if PREFILL_SPLIT_TOKENS < n_new <= PREFILL_RUNS_TOKENS and c.head_dim == 128:
+            blocks = (n_new + 127) // 128 * c.num_q_heads
+            runs = min(2 * self.cus // blocks, 16, PREFILL_RUN_TOKEN_RUNS // n_new)
+            return runs if runs > 1 else 0
+        return 0
 
     def run(self, out, q, kv, n_new, cache_len, stream=None):
         c = self.config

@@ -62,10 +62,11 @@ T* dev_alloc(size_t n) {
 }
 
 int run_case(BackendKind kind, const char* name) {
-    const int   L = 2, S = 256, Hq = 24, Hkv = 8, D = 128;
-    // chunk of 29: the flash prefill; chunk of 4: AdaptiveAttention's split-K
-    // prefill of a few tokens; then one-token decode steps.
-    const int   prefill = 37, chunk = 29, small = 4, steps = 5;
+    const int   L = 2, S = 512, Hq = 24, Hkv = 8, D = 128;
+    // Chunks of 300 (the flash prefill), 200 (AdaptiveAttention's flash
+    // prefill over key runs), 4 (its split-K decode route for a few tokens),
+    // then one-token decode steps.
+    const int   prefill = 300, chunk = 200, small = 4, steps = 5;
     const float scale = 1.0f / std::sqrt(static_cast<float>(D));
     const int   total = prefill + chunk + small + steps;
 

@@ -142,15 +142,16 @@ def test_prefill_split_rejects_bad_arguments():
                                    k, s, s, part, 4, 2, int_dev(0), hq, hkv, 32, 0.1)
 
 
-@pytest.mark.parametrize("n_new", [2, 128, 129])
+@pytest.mark.parametrize("n_new", [2, 128, 129, 256, 257])
 def test_adaptive_backend_routes_small_prefill(n_new):
-    """AdaptiveAttention.run: 2..128 tokens take the split-K prefill over the
-    backend's scratch, 129 the flash prefill; both match the oracle."""
+    """AdaptiveAttention.run: 2..128 tokens take the split-K decode route over
+    the backend's scratch, 129..256 the flash prefill over key runs, 257 the
+    flash prefill; all match the oracle."""
     hq, hkv, d, clen = 32, 8, 128, 3000
     scale = np.float32(1.0 / np.sqrt(d))
     q, k8, v8, ks, vs = inputs(n_new, clen, hq, hkv, d, 500 + n_new)
     be = R.AdaptiveAttention(R.AttnConfig.for_heads(hq, hkv, d))
-    assert (be._split_prefill_splits(n_new) > 0) == (n_new <= R.ops.PREFILL_SPLIT_TOKENS)
+    assert (be._split_prefill_splits(n_new) > 0) == (n_new <= R.ops.PREFILL_RUNS_TOKENS)
     kv = R.KVView(u8_dev(k8), u8_dev(v8), f32_dev(ks), f32_dev(vs))
     out = torch.empty((n_new, hq, d), dtype=torch.bfloat16, device=DEV)
     step(f"adaptive run n_new={n_new} clen={clen}")
