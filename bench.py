@@ -779,8 +779,8 @@ def main() -> int:
             "unit": "us per call", "points": few,
             "workload": "32Q/8KV head_dim 128: n_new = 4 / 16 / 128 / 256 / 512 tokens after 8192 / 32768 "
                         "cached keys; the flash prefill kernel vs AdaptiveAttention.run "
-                        "(split-K decode over (token block, kv head) units for 2..128 tokens, the "
-                        "flash prefill over key runs for 129..256); 512 tokens through "
+                        "(split-K decode over (token block, kv head) units for 2..80 tokens, the "
+                        "flash prefill over key runs for 81..256); 512 tokens through "
                         "rth_attn_prefill_split (key runs, ~2 rounds of workgroups)"},
         "decode_step_unfused": {
             "value": round(dec["unfused_value"], 1), "unit": "GB/s",

@@ -162,10 +162,10 @@ int rth_attn_prefill(uint16_t* out, const uint16_t* q, const uint8_t* k,
  * verification, prefill chunks), instead of one workgroup per q tile
  * streaming every key (reference flash_prefill.cu:34-241 walks all keys
  * serially per tile: n_new = 4 at 32K keys costs ~50x a decode step).
- * n_new <= 128, or head_dim != 128: the decode split kernel over (block of
+ * n_new <= 80, or head_dim != 128: the decode split kernel over (block of
  * tokens, kv head) units, token t over the first *cache_len + t + 1 keys
  * (shapes of the MFMA decode kernel, rth_decode_path == RTH_DECODE_MFMA:
- * head_dim 64 / 128 / 256; n_new <= 256). n_new > 128 at head_dim 128: the
+ * head_dim 64 / 128 / 256; n_new <= 256). n_new > 80 at head_dim 128: the
  * flash prefill with each (row block, q head) split over num_splits runs of
  * key tiles. Both end in the decode merge. n_new's K/V must already be in the
  * cache (as for rth_attn_prefill). partial: rth_split_scratch_floats(n_new *

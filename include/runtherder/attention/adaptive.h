@@ -5,12 +5,12 @@
 // the reference's fixed 32. Calls of 2 .. kPrefillSplitTokens tokens on shapes
 // the MFMA decode kernel serves run rth_attn_prefill_split over the same
 // scratch with num_splits / (2 n_new) splits (no reference counterpart: a few
-// tokens after a long cache as split-K decode; 16 / 64 / 128 tokens after 8K
-// keys 209 / 199 / 186 -> 18 / 35 / 57 us per call, at an empty cache up to
-// ~2.5 us slower), and at head_dim 128 calls of up to kPrefillRunsTokens
-// tokens run it as the flash prefill over key runs (256 tokens after 8K / 32K
-// keys 186 / 830 -> 67 / 179 us; at an empty cache 14 -> 27 us). For those
-// the scratch holds kPrefillRunTokenRuns token-runs (34 MB at 32 q heads).
+// tokens after a long cache as split-K decode; 16 / 64 tokens after 8K keys
+// 209 / 199 -> 18 / 34 us per call, at an empty cache up to ~2 us slower),
+// and at head_dim 128 calls of up to kPrefillRunsTokens tokens run it as the
+// flash prefill over key runs (128 / 256 tokens after 32K keys 828 / 830 ->
+// 98 / 187 us; at an empty cache 11 / 14 -> 19 / 27 us). For those the
+// scratch holds kPrefillRunTokenRuns token-runs (34 MB at 32 q heads).
 #pragma once
 
 #include <runtherder/attention/backend.h>
@@ -74,7 +74,7 @@ public:
 
     [[nodiscard]] int num_splits() const noexcept { return num_splits_; }
 
-    static constexpr int kPrefillSplitTokens  = 128;
+    static constexpr int kPrefillSplitTokens  = 80;
     static constexpr int kPrefillRunsTokens   = 256;
     static constexpr int kPrefillRunTokenRuns = 2048;
 

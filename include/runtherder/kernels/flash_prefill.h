@@ -38,7 +38,7 @@ inline void flash_prefill_bf16(__hip_bfloat16*       out,
 }
 
 // No reference counterpart: the same attention split over the keys
-// (rth_attn_prefill_split): up to 128 tokens as split-K decode over (token
+// (rth_attn_prefill_split): up to 80 tokens as split-K decode over (token
 // block, kv head) units, beyond as the flash prefill over num_splits key runs
 // per (row block, q head); partial holds flash_split_scratch_floats(n_new *
 // num_q_heads, head_dim, num_splits) floats.

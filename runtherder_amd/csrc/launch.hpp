@@ -65,7 +65,7 @@ hipError_t flash_decode_launch(uint16_t* out, const uint16_t* q,
 // heads: the shapes decode_mfma_supported accepts; partial holds
 // decode_scratch_floats(n_new * Hq, D, num_splits) floats.
 constexpr int kPrefillSplitMaxTokens       = 4096;   // rth_attn_prefill_split
-constexpr int kPrefillSplitDecodeTokens    = 128;    // above: the flash prefill over key runs
+constexpr int kPrefillSplitDecodeTokens    = 80;     // above: the flash prefill over key runs
 constexpr int kPrefillSplitDecodeMaxTokens = 256;    // the decode kernel's route at D != 128
 hipError_t flash_prefill_split_launch(uint16_t* out, const uint16_t* q, const uint8_t* k,
                                      const uint8_t* v, const float* k_scale,

@@ -195,7 +195,7 @@ def flash_prefill_split_bf16(out, q, k, v, k_scale, v_scale, partial, num_splits
                              stream=None):
     """flash_prefill_bf16 split over the keys, for calls after a long cache
     (no reference counterpart; the reference walks every key serially per q
-    tile, flash_prefill.cu:34-241): up to 128 tokens as split-K decode over
+    tile, flash_prefill.cu:34-241): up to 80 tokens as split-K decode over
     (token block, kv head) units, beyond (head_dim 128) the flash prefill over
     num_splits key runs per (row block, q head), both merged by the decode
     merge. partial: flash_split_scratch_floats(n_new * num_q_heads, head_dim,
@@ -443,7 +443,7 @@ class AttentionBackend:
         raise NotImplementedError
 
 
-PREFILL_SPLIT_TOKENS = 128
+PREFILL_SPLIT_TOKENS = 80
 PREFILL_RUNS_TOKENS = 256
 PREFILL_RUN_TOKEN_RUNS = 2048
 
@@ -454,13 +454,12 @@ class AdaptiveAttention(AttentionBackend):
     device's (kv head, split) fill count. Calls of 2..PREFILL_SPLIT_TOKENS
     tokens on shapes the MFMA decode kernel serves take the split-K prefill
     (flash_prefill_split_bf16) over the same scratch, with num_splits //
-    (2 n_new) splits (no reference counterpart: per call, 16 / 64 / 128
-    tokens after 8K keys 209 / 199 / 186 -> 18 / 35 / 57 us; at an empty
-    cache up to ~2.5 us slower); at head_dim 128, calls of up to
-    PREFILL_RUNS_TOKENS tokens take it as the flash prefill over key runs
-    (256 tokens after 8K / 32K keys 186 / 830 -> 67 / 179 us; at an empty
-    cache 14 -> 27 us), for which the scratch holds PREFILL_RUN_TOKEN_RUNS
-    token-runs."""
+    (2 n_new) splits (no reference counterpart: per call, 16 / 64 tokens
+    after 8K keys 209 / 199 -> 18 / 34 us; at an empty cache up to ~2 us
+    slower); at head_dim 128, calls of up to PREFILL_RUNS_TOKENS tokens take
+    it as the flash prefill over key runs (128 / 256 tokens after 32K keys
+    828 / 830 -> 98 / 187 us; at an empty cache 11 / 14 -> 19 / 27 us), for
+    which the scratch holds PREFILL_RUN_TOKEN_RUNS token-runs."""
 
     def __init__(self, config: AttnConfig, num_splits: int | None = None, device="cuda"):
         self.config = config

@@ -142,10 +142,10 @@ def test_prefill_split_rejects_bad_arguments():
                                    k, s, s, part, 4, 2, int_dev(0), hq, hkv, 32, 0.1)
 
 
-@pytest.mark.parametrize("n_new", [2, 128, 129, 256, 257])
+@pytest.mark.parametrize("n_new", [2, 80, 81, 256, 257])
 def test_adaptive_backend_routes_small_prefill(n_new):
-    """AdaptiveAttention.run: 2..128 tokens take the split-K decode route over
-    the backend's scratch, 129..256 the flash prefill over key runs, 257 the
+    """AdaptiveAttention.run: 2..80 tokens take the split-K decode route over
+    the backend's scratch, 81..256 the flash prefill over key runs, 257 the
     flash prefill; all match the oracle."""
     hq, hkv, d, clen = 32, 8, 128, 3000
     scale = np.float32(1.0 / np.sqrt(d))
