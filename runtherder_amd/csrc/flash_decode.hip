@@ -1520,6 +1520,9 @@ __global__ __launch_bounds__(kCombineThreads) void flash_decode_combine_kernel(
         const int tiles = (n_keys + 63) / 64;
         const int per   = max((tiles + num_splits - 1) / num_splits, run_min);
         n_eff           = (tiles + per - 1) / per;
+        if (n_eff == 1) {   // run 0 stored the output itself
+            return;
+        }
     }
     float     M       = -INFINITY;
     for (int s0 = 0;; s0 += 4 * kWave) {

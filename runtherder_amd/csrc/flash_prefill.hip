@@ -240,7 +240,9 @@ constexpr int waitcnt_vm(int n) {
 // ([rows, S] m, [rows, S] l, [rows, S, D] O, rows t * Hq + h) for the decode
 // merge; a row with no key in the run stores m = -inf, l = 0 and, in a
 // workgroup that has keys, O = 0 (a workgroup without keys leaves O unwritten;
-// the merge drops slots with m = -inf).
+// the merge drops slots with m = -inf). When run 0 holds every key (at most
+// kPartMinTiles tiles in all), it stores the normalized output instead and
+// the merge returns at once.
 constexpr int kPartMinTiles = 8;   // a run's minimum: short caches use few runs
 template <int kWaves, bool kPaged, bool kSplit = false, bool kEarly = false, bool kPart = false>
 __global__ __launch_bounds__(kWaves * kWave, kSplit ? 1 : 2) void flash_prefill_kernel(
@@ -304,16 +306,18 @@ __global__ __launch_bounds__(kWaves * kWave, kSplit ? 1 : 2) void flash_prefill_
     const int last    = min(q0 + kBM, n_new) - 1;
     const int n_tiles = min((total + kBN - 1) / kBN, (clen + last) / kBN + 1);
     // kPart: this workgroup's run of key tiles [kt_lo, kt_hi).
-    [[maybe_unused]] int kt_lo = 0;
-    [[maybe_unused]] int kt_hi = 0;
+    [[maybe_unused]] int  kt_lo   = 0;
+    [[maybe_unused]] int  kt_hi   = 0;
+    [[maybe_unused]] bool one_run = false;   // kPart: run 0 holds every key
     if constexpr (kPart) {
-        const int per = max(((total + kBN - 1) / kBN + num_splits - 1) / num_splits,
-                            kPartMinTiles);
-        kt_lo         = static_cast<int>(blockIdx.y) * per;
-        kt_hi         = min(kt_lo + per, n_tiles);
+        const int tiles_all = (total + kBN - 1) / kBN;
+        const int per       = max((tiles_all + num_splits - 1) / num_splits, kPartMinTiles);
+        one_run             = tiles_all <= per;
+        kt_lo               = static_cast<int>(blockIdx.y) * per;
+        kt_hi               = min(kt_lo + per, n_tiles);
         if (kt_hi <= kt_lo) {   // no key of this run for any row of the block: m, l only
             const int r = q0 + tid;
-            if (tid < kBM && r < n_new) {
+            if (!one_run && tid < kBM && r < n_new) {
                 const int64_t rows = static_cast<int64_t>(n_new) * hq;
                 const int64_t slot = (static_cast<int64_t>(r) * hq + qh) * num_splits +
                                      static_cast<int64_t>(blockIdx.y);
@@ -921,7 +925,9 @@ __global__ __launch_bounds__(kWaves * kWave, kSplit ? 1 : 2) void flash_prefill_
     }
 
     const float l_tot = wave_xor_sum(l_run, 32);
-    if constexpr (kPart) {
+    // kPart with a single live run (short caches): run 0 stores the output
+    // itself, as the plain kernel does, and the merge skips the call.
+    if (kPart && !one_run) {
         if (my_q < n_new) {
             const int64_t rows   = static_cast<int64_t>(n_new) * hq;
             const int64_t slot   = (static_cast<int64_t>(my_q) * hq + qh) * num_splits +

@@ -57,6 +57,9 @@ CASES = [
     # past the cache, more runs than tiles, one run, ragged row blocks).
     (100, 3000, 32, 8, 128, 4), (300, 5000, 24, 8, 128, 8), (1000, 200, 32, 8, 128, 3),
     (129, 0, 8, 1, 128, 16), (517, 7777, 16, 4, 128, 5), (256, 3000, 32, 8, 128, 1),
+    # all keys in run 0 (8 tiles: it stores the output itself) and one key
+    # tile past it.
+    (250, 200, 32, 8, 128, 8), (300, 250, 32, 8, 128, 8),
 ]
 
 
