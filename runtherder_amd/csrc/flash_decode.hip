@@ -37,7 +37,11 @@
 //  * A second small kernel merges the splits of every (q head, 16-wide d
 //    slice): the head maximum from the m row, then weighted sums over a
 //    strided subset of splits per thread, lane exchanges, one LDS step. The scratch layout is the reference's ([Hq,S] m, [Hq,S]
-//    l, [Hq,S,D] acc); it needs no initialization.
+//    l, [Hq,S,D] acc); it needs no initialization. A whole-row variant
+//    (one workgroup per row) merges calls of many rows and few splits.
+//  * The same split kernel serves a causal prefill of a few tokens after
+//    the cache (flash_decode_multi_kernel): blocks of tokens share a virtual
+//    kv head's MFMA columns, each column with its own key limit.
 //
 // Split si holds an even share of the kTileKeys-key tiles over the keys; the
 // merge folds the first n_eff = min(splits, tiles) slots. n_keys =
