@@ -44,6 +44,10 @@
 //    wave in its softmax or P V runs at a higher issue priority than one in
 //    its score MFMAs; the 4-wave workgroups weave the next tile's copies and
 //    V staging between their own MFMAs.
+//  * Key runs (flash_prefill_keysplit_launch, kPart): for chunks after a long
+//    cache, each (row block, q head) of the 4-wave kernel is split over
+//    gridDim.y workgroups, each walking one run of key tiles and storing
+//    partials in the split-K decode layout for the decode merge.
 #include "device_common.hpp"
 #include "launch.hpp"
 
