@@ -713,7 +713,7 @@ def main() -> int:
         return eager_kernels(torch, R, stream, args)
     if args.sweep == "few":
         for p in bench_few_token_prefill(torch, R, stream):
-            print(json.dumps({"prefill_few_tokens": p}), flush=True)
+            print(json.dumps({"prefill_after_long_cache": p}), flush=True)
         return 0
     if args.sweep:
         if args.sweep != "prefill":
@@ -775,7 +775,7 @@ def main() -> int:
         "rope_append": dict(ra, workload="config4 shapes: RoPE(q,k) + K/V FP8 append (and the "
                                          "Qwen3 q/k RMSNorm before it), fused entries vs the "
                                          "unfused launch sequences"),
-        "prefill_few_tokens": {
+        "prefill_after_long_cache": {
             "unit": "us per call", "points": few,
             "workload": "32Q/8KV head_dim 128: n_new = 4 / 16 / 128 / 256 / 512 tokens after 8192 / 32768 "
                         "cached keys; the flash prefill kernel vs AdaptiveAttention.run "
